@@ -1,0 +1,227 @@
+"""Benchmark of the fused Conv2D hot path on one MI355X (BASELINE.json metric: fused FP16 conv TFLOP/s and % of
+the MFMA peak per config; us/call next to the host CPU reference).
+
+A step is one Conv2D::forward call through the unchanged plan API (plan-cache lookup, argument validation,
+fused repack dispatch, MFMA implicit GEMM with the bias+ReLU epilogue, split-K reduce when the selected
+kernel splits), issued back-to-back from C++ on one stream with inputs already resident in HBM. `value` is
+config 2 (FP16 3x3, N=32 C=256 14x14 K=256): TFLOP/s = 2*M*N*K / (time per step).
+The other GPU configs (1x1, 7x7 stem, BF16 split-K) are reported under "configs" with the same protocol.
+
+roofline: the dominant kernel (the MFMA implicit GEMM) timed with HIP events recorded on its own stream around
+each launch, algorithmic FLOPs per launch / average launch duration against the dense FP16 MFMA peak.
+cpu_baseline: the oracle's C restatement of the reference's cpu_conv2d_reference (OpenMP, double accumulation)
+on the same quantized inputs, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cuda-inference_amd"))
+
+PEAK_FP16_TFLOPS = 2516.6  # MI355X dense FP16/BF16 MFMA (256 CUs x 4096 FLOP/clk x 2.4 GHz)
+PEAK_HBM_GBS = 8000.0
+SEED = 0x1234ABCD
+
+CONFIGS = {
+    "c2_fp16_3x3": dict(batch=32, in_channels=256, in_h=14, in_w=14, out_channels=256, kernel_h=3, kernel_w=3,
+                        stride_h=1, stride_w=1, pad_h=1, pad_w=1, precision="fp16"),
+    "c3_fp16_1x1": dict(batch=64, in_channels=256, in_h=28, in_w=28, out_channels=1024, kernel_h=1, kernel_w=1,
+                        stride_h=1, stride_w=1, pad_h=0, pad_w=0, precision="fp16"),
+    "c4_fp16_7x7s2_stem": dict(batch=64, in_channels=3, in_h=224, in_w=224, out_channels=64, kernel_h=7, kernel_w=7,
+                               stride_h=2, stride_w=2, pad_h=3, pad_w=3, precision="fp16"),
+    "c5_bf16_3x3_splitk": dict(batch=8, in_channels=512, in_h=7, in_w=7, out_channels=512, kernel_h=3, kernel_w=3,
+                               stride_h=1, stride_w=1, pad_h=1, pad_w=1, precision="bf16"),
+}
+HEADLINE = "c2_fp16_3x3"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def compulsory_bytes(p) -> float:
+    e = p.esize
+    return float((np.prod(p.x_shape()) + np.prod(p.w_shape()) + np.prod(p.y_shape()) + p.out_channels) * e)
+
+
+def run_config(gie, name, cfg, steps, warmup, stream, tune_cache):
+    p = gie.Problem(**cfg, has_bias=True, relu=True)
+    x, w, b = gie.make_host_data(p, SEED, "uniform", "benchmark")
+    t = gie.ConvTensors(p, x, w, b)
+    # pick the kernel: autotuned (validated against the GPU double reference, cached), else the cost model
+    opts = dict(autotune=True, cache_path=tune_cache)
+    kernel, source, _ = gie.select(p, **opts)
+    ws = gie.DeviceBuffer(gie.workspace_size(p, **opts))
+    # correctness of the exact call being timed, against the library's GPU double reference
+    gie.forward(p, t, ws, stream, **opts)
+    stream.sync()
+    y = t.y().astype(np.float64)
+    ref, _ = gie.gpu_reference(p, t)
+    ref = ref.astype(np.float64)
+    if p.precision == "bf16":
+        ref_r = (gie.storage_to_float(gie.host_to_storage(ref.astype(np.float32), "bf16"), "bf16")).astype(np.float64)
+    else:
+        ref_r = ref
+    rel_l2 = float(np.linalg.norm(y - ref_r) / np.linalg.norm(ref_r))
+    max_abs = float(np.abs(y - ref).max())
+    # timed region: exactly `steps` forward calls between two events on the stream
+    gie.forward_n(p, t, ws, stream, warmup, **opts)
+    stream.sync()
+    e0, e1 = gie.Event(), gie.Event()
+    gie.synchronize()
+    e0.record(stream)
+    gie.forward_n(p, t, ws, stream, steps, **opts)
+    e1.record(stream)
+    e1.sync()
+    gie.synchronize()
+    ms = e0.elapsed_ms(e1)
+    us_call = ms * 1e3 / steps
+    flops = p.flops()
+    tflops = flops / (us_call * 1e-6) / 1e12
+    # per-stage device time (events on the launch stream around each kernel), same plan and buffers
+    plan = gie.Plan(p, kernel)
+    stages = plan.time_stages(t, ws, stream, iters=max(50, min(steps, 400)))
+    gemm_tflops = flops / (stages["gemm_us"] * 1e-6) / 1e12
+    cb = compulsory_bytes(p)
+    ai = flops / cb
+    roof_tflops = min(PEAK_FP16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
+    cp = (p.in_channels + 7) // 8 * 8
+    repack_bytes = float((np.prod(p.x_shape()) + np.prod(p.w_shape())) * 2 +
+                         (p.batch * p.in_h * p.in_w + p.out_channels * p.kernel_h * p.kernel_w) * cp * 2)
+    desc = gie.kernel_describe(kernel)
+    split = desc.get("split_k", 1)
+    reduce_bytes = float(split * np.prod(p.y_shape()) * 4 + np.prod(p.y_shape()) * 2) if split > 1 else 0.0
+    out = {
+        "kernel": kernel, "selection": source, "gemm_view": {"M": p.gemm_m, "N": p.gemm_n, "K": p.gemm_k},
+        "gflop": flops / 1e9, "us_per_call": us_call, "tflops": tflops,
+        "pct_of_fp16_peak": 100.0 * tflops / PEAK_FP16_TFLOPS,
+        "roofline_tflops": roof_tflops, "roofline_fraction": tflops / roof_tflops,
+        "bound": "mfma" if ai * PEAK_HBM_GBS / 1e3 >= PEAK_FP16_TFLOPS else "hbm",
+        "compulsory_mb": cb / 1e6, "arith_intensity": ai,
+        "stage_us": stages, "gemm_kernel_tflops": gemm_tflops,
+        "repack_gbs": repack_bytes / (stages["repack_us"] * 1e-6) / 1e9 if stages["repack_us"] > 0 else None,
+        "reduce_gbs": reduce_bytes / (stages["reduce_us"] * 1e-6) / 1e9 if stages["reduce_us"] > 0 else None,
+        "split_k": split, "rel_l2": rel_l2, "max_abs": max_abs,
+        "parity_ok": bool(rel_l2 <= 1e-3 and max_abs <= 2e-2),
+    }
+    return p, t, out
+
+
+def cpu_baseline(p, t, budget_s: float):
+    """Oracle CPU reference (C, OpenMP, double accumulation) on the same quantized inputs, bounded in time."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    c = O.Conv(p.batch, p.in_channels, p.in_h, p.in_w, p.out_channels, p.kernel_h, p.kernel_w, p.stride_h,
+               p.stride_w, p.pad_h, p.pad_w, has_bias=True, relu=True, precision=p.precision)
+    x, w, b = O.make_data(c, SEED, O.UNIFORM, O.SCALING_BENCH)
+    cores = len(os.sched_getaffinity(0))
+    times = []
+    t_end = time.time() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        O.conv2d(c, x, w, b, threads=cores)
+        times.append(time.perf_counter() - t0)
+        if time.time() > t_end or len(times) >= 50:
+            break
+    med = float(np.median(times))
+    return {"value": p.flops() / med / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "us_per_call": med * 1e6,
+            "sample": f"full config-2 workload ({p.flops() / 1e9:.2f} GFLOP) x {len(times)} runs, median; "
+                      f"oracle/gie_oracle.c cpu_conv2d_reference restatement, {cores} OpenMP threads",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def load_traffic(kernel_name: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", "traffic_c2_fp16_3x3.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return d.get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--configs", default="all", help="'all' or a comma list of config names")
+    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--tune-cache", default=os.path.join(ROOT, "gpurun_out", "bench_tune_cache.json"))
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the Conv2D library is a "
+              "single-GPU operator; see DESIGN.md for how it would shard by batch).", file=sys.stderr)
+        sys.exit(2)
+
+    import gie
+    gie.check(gie.capi().gie_set_device(0), "hipSetDevice")
+    os.makedirs(os.path.dirname(args.tune_cache), exist_ok=True)
+    stream = gie.Stream()
+    names = list(CONFIGS) if args.configs == "all" else args.configs.split(",")
+    if HEADLINE not in names:
+        names.insert(0, HEADLINE)
+    results = {}
+    head = None
+    for name in names:
+        log(f"[bench] {name}: tuning + timing")
+        steps = args.steps if name == HEADLINE else max(100, args.steps // 4)
+        p, t, r = run_config(gie, name, CONFIGS[name], steps, args.warmup if name == HEADLINE else 50, stream,
+                             args.tune_cache)
+        log(f"[bench] {name}: {r['kernel']} {r['us_per_call']:.2f} us/call {r['tflops']:.1f} TFLOP/s "
+            f"(gemm {r['stage_us']['gemm_us']:.2f} us, repack {r['stage_us']['repack_us']:.2f} us) "
+            f"rel_l2={r['rel_l2']:.2e}")
+        results[name] = r
+        if name == HEADLINE:
+            head = (p, t)
+    hr = results[HEADLINE]
+    p, t = head
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline (oracle) on the host")
+        cpu = cpu_baseline(p, t, args.cpu_budget_s)
+    gemm_us = hr["stage_us"]["gemm_us"]
+    achieved = p.flops() / (gemm_us * 1e-6) / 1e12
+    line = {
+        "metric": "fused FP16 conv TFLOP/s (conv+bias+ReLU through Conv2D::forward, incl. repack)",
+        "value": hr["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": hr["us_per_call"] / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (SplitMix64 seed 0x1234ABCD; x U[-1,1], w U[-1,1]/sqrt(K), b U[-0.1,0.1])",
+        "config": {"workload": "BASELINE configs[1]: FP16 NCHW 3x3 conv N=32 C=256 H=W=14 K=256 s1 p1 + bias + ReLU",
+                   "gemm_view": hr["gemm_view"], "kernel": hr["kernel"], "selection": hr["selection"],
+                   "pct_of_fp16_peak": hr["pct_of_fp16_peak"], "us_per_call": hr["us_per_call"]},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_FP16_TFLOPS, "traffic": load_traffic(hr["kernel"]),
+                     "kernel": "igemm_kernel (MFMA implicit GEMM)", "avg_launch_us": gemm_us,
+                     "flop_per_launch": p.flops()},
+        "cpu_baseline": cpu,
+        "parity": {"rel_l2": hr["rel_l2"], "max_abs": hr["max_abs"], "ok": hr["parity_ok"],
+                   "against": "library GPU double reference on the timed call's inputs"},
+        "configs": results,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

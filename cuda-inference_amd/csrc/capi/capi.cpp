@@ -1,0 +1,600 @@
+// Flat C-ABI over the gie:: C++ API (include/gie_capi.h). Each function catches every exception and turns it
+// into a status code plus a thread-local message.
+#include "gie_capi.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gpu_inference/autotuner.h"
+#include "gpu_inference/build_info.h"
+#include "gpu_inference/conv2d.h"
+#include "gpu_inference/dispatcher.h"
+#include "gpu_inference/execution_plan.h"
+#include "gpu_inference/hip_graph.h"
+#include "gpu_inference/perf_model.h"
+#include "gpu_inference/reference.h"
+#include "gpu_inference/testing.h"
+#include "gpu_inference/timing.h"
+
+using namespace gie;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return 0;
+  } catch (const Error& e) {
+    g_last_error = e.what();
+    return int(e.code());
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return int(StatusCode::kInternal);
+  } catch (...) {
+    g_last_error = "unknown exception";
+    return int(StatusCode::kInternal);
+  }
+}
+
+void copy_str(const std::string& s, char* buf, size_t n) {
+  if (!buf || n == 0) return;
+  const size_t k = std::min(n - 1, s.size());
+  std::memcpy(buf, s.data(), k);
+  buf[k] = '\0';
+}
+
+ConvProblem to_problem(const gie_problem* p) {
+  GIE_REQUIRE(p != nullptr, StatusCode::kInvalidArgument, "null problem");
+  ConvProblem pr;
+  pr.p.batch = p->batch;
+  pr.p.in_channels = p->in_channels;
+  pr.p.in_h = p->in_h;
+  pr.p.in_w = p->in_w;
+  pr.p.out_channels = p->out_channels;
+  pr.p.kernel_h = p->kernel_h;
+  pr.p.kernel_w = p->kernel_w;
+  pr.p.stride_h = p->stride_h;
+  pr.p.stride_w = p->stride_w;
+  pr.p.pad_h = p->pad_h;
+  pr.p.pad_w = p->pad_w;
+  pr.p.dilation_h = p->dilation_h;
+  pr.p.dilation_w = p->dilation_w;
+  pr.p.groups = p->groups;
+  GIE_REQUIRE(p->precision >= 0 && p->precision <= 3, StatusCode::kInvalidArgument, "bad precision");
+  pr.precision = static_cast<Precision>(p->precision);
+  pr.has_bias = p->has_bias != 0;
+  pr.activation = p->relu ? Activation::kReLU : Activation::kNone;
+  return pr;
+}
+
+Conv2DOptions to_options(const gie_options* o) {
+  Conv2DOptions opt;
+  if (!o) return opt;
+  GIE_REQUIRE(o->backend >= 0 && o->backend <= 6, StatusCode::kInvalidArgument, "bad backend");
+  opt.backend = static_cast<Backend>(o->backend);
+  if (o->kernel) opt.kernel = o->kernel;
+  opt.autotune = o->autotune != 0;
+  opt.force_retune = o->force_retune != 0;
+  if (o->cache_path) opt.cache_path = o->cache_path;
+  return opt;
+}
+
+ConstTensorRef to_cref(const gie_tensor* t) {
+  GIE_REQUIRE(t != nullptr, StatusCode::kInvalidArgument, "null tensor descriptor");
+  GIE_REQUIRE(t->dtype >= 0 && t->dtype <= 2, StatusCode::kInvalidArgument, "bad dtype");
+  return {t->data, static_cast<DataType>(t->dtype), {t->n, t->c, t->h, t->w}};
+}
+
+TensorRef to_ref(const gie_tensor* t) {
+  const ConstTensorRef c = to_cref(t);
+  return {const_cast<void*>(c.data), c.dtype, c.shape};
+}
+
+struct PlanHandle {
+  std::shared_ptr<ExecutionPlan> plan;
+};
+
+ExecutionPlan& plan_of(void* h) {
+  GIE_REQUIRE(h != nullptr, StatusCode::kInvalidArgument, "null plan handle");
+  return *static_cast<PlanHandle*>(h)->plan;
+}
+
+const KernelDesc& kernel_named(const char* name) {
+  GIE_REQUIRE(name != nullptr, StatusCode::kInvalidArgument, "null kernel name");
+  const KernelDesc* k = find_kernel(name);
+  GIE_REQUIRE(k != nullptr, StatusCode::kInvalidArgument, std::string("unknown kernel '") + name + "'");
+  return *k;
+}
+
+HipGraphExecutor::Enqueue chain_enqueue(int n, void* const* plans, const void* const* xs, const void* const* ws,
+                                        const void* const* biases, void* const* ys, void* const* wss,
+                                        const size_t* ws_bytes) {
+  GIE_REQUIRE(n > 0 && plans && xs && ws && ys, StatusCode::kInvalidArgument, "bad chain description");
+  std::vector<std::shared_ptr<ExecutionPlan>> ps;
+  for (int i = 0; i < n; ++i) {
+    GIE_REQUIRE(plans[i] != nullptr, StatusCode::kInvalidArgument, "null plan in chain");
+    ps.push_back(static_cast<PlanHandle*>(plans[i])->plan);
+  }
+  std::vector<const void*> vx(xs, xs + n), vw(ws, ws + n), vb(n, nullptr);
+  std::vector<void*> vy(ys, ys + n), vws(n, nullptr);
+  std::vector<size_t> vwb(n, 0);
+  for (int i = 0; i < n; ++i) {
+    if (biases) vb[i] = biases[i];
+    if (wss) vws[i] = wss[i];
+    if (ws_bytes) vwb[i] = ws_bytes[i];
+  }
+  return [=](hipStream_t s) {
+    for (int i = 0; i < n; ++i) ps[size_t(i)]->execute_unchecked(vx[i], vw[i], vb[i], vy[i], vws[i], vwb[i], s);
+  };
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gie_last_error(void) { return g_last_error.c_str(); }
+const char* gie_status_string(int status) { return to_string(static_cast<StatusCode>(status)); }
+
+int gie_validate_problem(const gie_problem* p) {
+  return guarded([&] { validate_problem(to_problem(p)); });
+}
+
+int gie_problem_key(const gie_problem* p, char* buf, size_t n) {
+  return guarded([&] { copy_str(to_problem(p).key(), buf, n); });
+}
+
+int gie_conv2d_forward(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                       const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
+                       const gie_options* opt) {
+  return guarded([&] {
+    const ConstTensorRef b = bias ? to_cref(bias) : ConstTensorRef{};
+    Conv2D::forward(to_cref(x), to_cref(w), bias ? &b : nullptr, to_problem(p), to_ref(y), workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream), to_options(opt));
+  });
+}
+
+int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                         const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
+                         const gie_options* opt, int count) {
+  return guarded([&] {
+    const ConstTensorRef b = bias ? to_cref(bias) : ConstTensorRef{};
+    const ConstTensorRef xr = to_cref(x), wr = to_cref(w);
+    const TensorRef yr = to_ref(y);
+    const ConvProblem pr = to_problem(p);
+    const Conv2DOptions o = to_options(opt);
+    for (int i = 0; i < count; ++i)
+      Conv2D::forward(xr, wr, bias ? &b : nullptr, pr, yr, workspace, workspace_bytes,
+                      static_cast<hipStream_t>(stream), o);
+  });
+}
+
+int gie_conv2d_workspace_size(const gie_problem* p, const gie_options* opt, size_t* bytes) {
+  return guarded([&] { *bytes = Conv2D::workspace_size(to_problem(p), to_options(opt)); });
+}
+
+int gie_conv2d_clear_plan_cache(void) {
+  return guarded([&] { Conv2D::clear_plan_cache(); });
+}
+
+int gie_plan_create(const gie_problem* p, const char* kernel_name, int device, void** plan) {
+  return guarded([&] {
+    GIE_REQUIRE(plan != nullptr, StatusCode::kInvalidArgument, "null output handle");
+    auto h = std::make_unique<PlanHandle>();
+    h->plan = ExecutionPlan::create(to_problem(p), kernel_named(kernel_name), device);
+    *plan = h.release();
+  });
+}
+
+int gie_plan_destroy(void* plan) {
+  return guarded([&] { delete static_cast<PlanHandle*>(plan); });
+}
+
+int gie_plan_workspace_bytes(void* plan, size_t* bytes) {
+  return guarded([&] { *bytes = plan_of(plan).workspace_bytes(); });
+}
+
+int gie_plan_kernel_name(void* plan, char* buf, size_t n) {
+  return guarded([&] { copy_str(plan_of(plan).kernel().name, buf, n); });
+}
+
+int gie_plan_execute(void* plan, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                     const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    const ConstTensorRef b = bias ? to_cref(bias) : ConstTensorRef{};
+    plan_of(plan).execute(to_cref(x), to_cref(w), bias ? &b : nullptr, to_ref(y), workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream));
+  });
+}
+
+int gie_plan_execute_unchecked(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    plan_of(plan).execute_unchecked(x, w, bias, y, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  });
+}
+
+int gie_plan_time(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                  size_t workspace_bytes, void* stream, int warmup, int samples, double min_sample_ms,
+                  double* stats7, int* inner) {
+  return guarded([&] {
+    ExecutionPlan& pl = plan_of(plan);
+    TimingOptions to;
+    to.warmup_iters = warmup;
+    to.samples = samples;
+    to.min_sample_ms = min_sample_ms;
+    const TimingStats t = time_stream_work(
+        [&](hipStream_t s) { pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s); },
+        static_cast<hipStream_t>(stream), to);
+    const double v[7] = {t.median_us, t.mean_us, t.min_us, t.max_us, t.p10_us, t.p90_us, t.stddev_us};
+    if (stats7) std::memcpy(stats7, v, sizeof(v));
+    if (inner) *inner = t.inner_iters;
+  });
+}
+
+int gie_plan_time_stages(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                         size_t workspace_bytes, void* stream, int iters, double* us3) {
+  return guarded([&] {
+    ExecutionPlan& pl = plan_of(plan);
+    GIE_REQUIRE(iters > 0 && us3, StatusCode::kInvalidArgument, "bad iteration count");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipEvent_t ev[4];
+    for (auto& e : ev) GIE_HIP_CHECK(hipEventCreate(&e));
+    struct G {
+      hipEvent_t* e;
+      ~G() {
+        for (int i = 0; i < 4; ++i) (void)hipEventDestroy(e[i]);
+      }
+    } guard{ev};
+    double acc[3] = {0, 0, 0};
+    for (int it = 0; it < iters; ++it) {
+      pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, ev);
+      GIE_HIP_CHECK(hipEventSynchronize(ev[3]));
+      float a = 0, b = 0, c = 0;
+      GIE_HIP_CHECK(hipEventElapsedTime(&a, ev[0], ev[1]));
+      GIE_HIP_CHECK(hipEventElapsedTime(&b, ev[1], ev[2]));
+      GIE_HIP_CHECK(hipEventElapsedTime(&c, ev[2], ev[3]));
+      acc[0] += a * 1e3;
+      acc[1] += b * 1e3;
+      acc[2] += c * 1e3;
+    }
+    for (int i = 0; i < 3; ++i) us3[i] = acc[i] / iters;
+  });
+}
+
+int gie_registry_count(void) {
+  int n = 0;
+  guarded([&] { n = int(kernel_registry().size()); });
+  return n;
+}
+
+int gie_registry_name(int index, char* buf, size_t n) {
+  return guarded([&] {
+    GIE_REQUIRE(index >= 0 && size_t(index) < kernel_registry().size(), StatusCode::kInvalidArgument, "bad index");
+    copy_str(kernel_registry()[size_t(index)].name, buf, n);
+  });
+}
+
+int gie_kernel_describe(const char* name, char* buf, size_t n) {
+  return guarded([&] {
+    const KernelDesc& k = kernel_named(name);
+    std::string s = "backend=" + std::string(to_string(k.backend)) + ",version=" + std::to_string(k.version) +
+                    ",threads=" + std::to_string(k.threads_per_block) + ",tile_m=" + std::to_string(k.tile_m) +
+                    ",tile_n=" + std::to_string(k.tile_n) + ",tile_k=" + std::to_string(k.tile_k) +
+                    ",launches=" + std::to_string(k.launches);
+    for (const auto& kv : k.params) s += "," + kv.first + "=" + std::to_string(kv.second);
+    copy_str(s, buf, n);
+  });
+}
+
+int gie_kernel_supports(const char* name, const gie_problem* p, int* ok, char* why, size_t why_n) {
+  return guarded([&] {
+    const KernelDesc& k = kernel_named(name);
+    std::string reason;
+    *ok = k.supports(to_problem(p), DeviceInfo::current(), &reason) ? 1 : 0;
+    copy_str(reason, why, why_n);
+  });
+}
+
+int gie_dispatch_select(const gie_problem* p, const gie_options* opt, char* kernel, size_t n, int* source,
+                        double* predicted_us) {
+  return guarded([&] {
+    const Selection sel = Dispatcher::select(to_problem(p), DeviceInfo::current(), to_options(opt));
+    copy_str(sel.kernel->name, kernel, n);
+    if (source) *source = int(sel.source);
+    if (predicted_us) *predicted_us = sel.predicted_us;
+  });
+}
+
+int gie_rank_by_model(const gie_problem* p, char* buf, size_t n, double* us, int max, int* count) {
+  return guarded([&] {
+    const ConvProblem pr = to_problem(p);
+    const DeviceInfo& dev = DeviceInfo::current();
+    const auto ranked = Dispatcher::rank_by_model(pr, dev, Dispatcher::compatible_kernels(pr, dev));
+    std::string names;
+    int i = 0;
+    for (const auto& r : ranked) {
+      if (i < max && us) us[i] = r.second;
+      if (!names.empty()) names += "\n";
+      names += r.first->name;
+      ++i;
+    }
+    copy_str(names, buf, n);
+    if (count) *count = int(ranked.size());
+  });
+}
+
+void gie_tune_options_default(gie_tune_options* o) {
+  if (!o) return;
+  const TuneOptions d;
+  o->warmup = d.timing.warmup_iters;
+  o->samples = d.timing.samples;
+  o->min_sample_ms = d.timing.min_sample_ms;
+  o->seed = d.seed;
+  o->validate = d.validate ? 1 : 0;
+  o->model_keep = d.model_keep;
+  o->max_candidates = d.max_candidates;
+  o->use_cache = d.use_cache ? 1 : 0;
+  o->force_retune = d.force_retune ? 1 : 0;
+  o->verbose = d.verbose ? 1 : 0;
+  o->cache_path = nullptr;
+}
+
+int gie_autotune(const gie_problem* p, const gie_tune_options* o, char* best, size_t n, double* best_us,
+                 double* search_seconds, int* counts6) {
+  return guarded([&] {
+    TuneOptions to;
+    if (o) {
+      to.timing.warmup_iters = o->warmup;
+      to.timing.samples = o->samples;
+      to.timing.min_sample_ms = o->min_sample_ms;
+      to.seed = o->seed;
+      to.validate = o->validate != 0;
+      to.model_keep = o->model_keep;
+      to.max_candidates = o->max_candidates;
+      to.use_cache = o->use_cache != 0;
+      to.force_retune = o->force_retune != 0;
+      to.verbose = o->verbose != 0;
+      if (o->cache_path) to.cache_path = o->cache_path;
+    }
+    const TuneResult r = Autotuner::tune(to_problem(p), DeviceInfo::current(), to);
+    copy_str(r.best_kernel, best, n);
+    if (best_us) *best_us = r.best_us;
+    if (search_seconds) *search_seconds = r.search_seconds;
+    if (counts6) {
+      int rej = 0, fail = 0, err = 0;
+      for (const auto& c : r.candidates) {
+        if (c.status.rfind("rejected", 0) == 0) ++rej;
+        else if (c.status.rfind("failed validation", 0) == 0) ++fail;
+        else if (c.status.rfind("error", 0) == 0) ++err;
+      }
+      const int v[6] = {r.candidates_total, r.candidates_measured, r.from_cache ? 1 : 0, rej, fail, err};
+      std::memcpy(counts6, v, sizeof(v));
+    }
+  });
+}
+
+int gie_tune_cache_key(const gie_problem* p, int scope_backend, char* buf, size_t n) {
+  return guarded([&] {
+    copy_str(TuneCache::make_key(to_problem(p), DeviceInfo::current(), static_cast<Backend>(scope_backend)), buf, n);
+  });
+}
+
+int gie_tune_cache_size(const char* path, size_t* size) {
+  return guarded([&] { *size = TuneCache(path ? path : "").size(); });
+}
+
+int gie_tune_cache_clear(const char* path) {
+  return guarded([&] { TuneCache(path ? path : "").clear(); });
+}
+
+int gie_estimate_kernel(const char* name, const gie_problem* p, double* out6, int* bound) {
+  return guarded([&] {
+    const DeviceInfo& dev = DeviceInfo::current();
+    DeviceCeilings c;
+    if (!load_cached_ceilings(dev.device, &c)) c = theoretical_ceilings(dev);
+    const Estimate e = estimate_kernel(to_problem(p), kernel_named(name), dev, c);
+    const double v[6] = {e.time_us, e.compute_us, e.memory_us, e.launch_us, e.tile_efficiency, e.wave_efficiency};
+    std::memcpy(out6, v, sizeof(v));
+    if (bound) *bound = int(e.bound);
+  });
+}
+
+int gie_measure_ceilings(int device, int use_cache, double* out3, int* measured) {
+  return guarded([&] {
+    const DeviceCeilings c = measure_ceilings(device, use_cache != 0);
+    out3[0] = c.fp16_tc_tflops;
+    out3[1] = c.bw_gbs;
+    out3[2] = c.launch_overhead_us;
+    if (measured) *measured = c.measured ? 1 : 0;
+  });
+}
+
+int gie_theoretical_ceilings(int device, double* out3) {
+  return guarded([&] {
+    const DeviceCeilings c = theoretical_ceilings(DeviceInfo::get(device));
+    out3[0] = c.fp16_tc_tflops;
+    out3[1] = c.bw_gbs;
+    out3[2] = c.launch_overhead_us;
+  });
+}
+
+int gie_gpu_reference(const gie_problem* p, const void* x, const void* w, const void* bias, float* y, float* scale,
+                      void* stream) {
+  return guarded([&] { gpu_conv2d_reference(to_problem(p), x, w, bias, y, scale, static_cast<hipStream_t>(stream)); });
+}
+
+int gie_cpu_reference(const gie_problem* p, const float* x, const float* w, const float* bias, float* y,
+                      float* scale) {
+  return guarded([&] {
+    ReferenceOutput out;
+    const ConvProblem pr = to_problem(p);
+    cpu_conv2d_reference(pr, x, w, bias, &out);
+    std::memcpy(y, out.y.data(), out.y.size() * 4);
+    std::memcpy(scale, out.scale.data(), out.scale.size() * 4);
+  });
+}
+
+int gie_make_host_data(const gie_problem* p, uint64_t seed, int dist, int scaling, float* x, float* w, float* bias) {
+  return guarded([&] {
+    GIE_REQUIRE(dist >= 0 && dist <= 3 && (scaling == 0 || scaling == 1), StatusCode::kInvalidArgument,
+                "bad distribution or scaling");
+    const ConvProblem pr = to_problem(p);
+    validate_problem(pr);
+    const Conv2DParams& q = pr.p;
+    Rng rng(seed);
+    const int64_t nx = q.input_shape().numel(), nw = q.weight_shape().numel();
+    auto draw = [&]() -> float {
+      switch (dist) {
+        case 1: return rng.normal();
+        case 2: return rng.uniform() < 0.7 ? 0.f : rng.uniform(-2.f, 2.f);
+        case 3: return rng.uniform(0.f, 1.f);
+        default: return rng.uniform(-1.f, 1.f);
+      }
+    };
+    const float k = float(q.gemm_k());
+    const float wscale = scaling == 1 ? 1.0f / std::sqrt(k) : std::sqrt(3.0f / k);
+    const float blim = scaling == 1 ? 0.1f : 1.0f;
+    for (int64_t i = 0; i < nx; ++i) x[i] = quantize_to(pr.precision, draw());
+    for (int64_t i = 0; i < nw; ++i) w[i] = quantize_to(pr.precision, draw() * wscale);
+    const bool half = pr.dtype() != DataType::kFloat32;
+    for (int i = 0; i < q.out_channels; ++i) {
+      const float v = rng.uniform(-blim, blim);
+      bias[i] = half ? quantize_to(pr.precision, v) : v;
+    }
+  });
+}
+
+int gie_device_describe(int device, char* buf, size_t n) {
+  return guarded([&] { copy_str(DeviceInfo::get(device).describe(), buf, n); });
+}
+
+int gie_device_arch(int device, char* buf, size_t n) {
+  return guarded([&] { copy_str(DeviceInfo::get(device).gcn_arch, buf, n); });
+}
+
+int gie_device_cu_count(int device, int* cus) {
+  return guarded([&] { *cus = DeviceInfo::get(device).sm_count; });
+}
+
+int gie_build_fingerprint(char* buf, size_t n) {
+  return guarded([&] { copy_str(build_info().source_fingerprint, buf, n); });
+}
+
+int gie_graph_create(void** graph) {
+  return guarded([&] { *graph = new HipGraphExecutor(); });
+}
+
+int gie_graph_destroy(void* graph) {
+  return guarded([&] { delete static_cast<HipGraphExecutor*>(graph); });
+}
+
+int gie_graph_capture_chain(void* graph, int n, void* const* plans, const void* const* xs, const void* const* ws,
+                            const void* const* biases, void* const* ys, void* const* wss, const size_t* ws_bytes) {
+  return guarded([&] {
+    GIE_REQUIRE(graph != nullptr, StatusCode::kInvalidArgument, "null graph");
+    static_cast<HipGraphExecutor*>(graph)->capture(chain_enqueue(n, plans, xs, ws, biases, ys, wss, ws_bytes));
+  });
+}
+
+int gie_graph_recapture_chain(void* graph, int n, void* const* plans, const void* const* xs, const void* const* ws,
+                              const void* const* biases, void* const* ys, void* const* wss, const size_t* ws_bytes,
+                              int* updated_in_place) {
+  return guarded([&] {
+    GIE_REQUIRE(graph != nullptr, StatusCode::kInvalidArgument, "null graph");
+    const bool up =
+        static_cast<HipGraphExecutor*>(graph)->recapture_update(chain_enqueue(n, plans, xs, ws, biases, ys, wss, ws_bytes));
+    if (updated_in_place) *updated_in_place = up ? 1 : 0;
+  });
+}
+
+int gie_graph_launch(void* graph, void* stream) {
+  return guarded([&] {
+    GIE_REQUIRE(graph != nullptr, StatusCode::kInvalidArgument, "null graph");
+    static_cast<HipGraphExecutor*>(graph)->launch(static_cast<hipStream_t>(stream));
+  });
+}
+
+int gie_graph_node_count(void* graph, size_t* nodes) {
+  return guarded([&] {
+    GIE_REQUIRE(graph != nullptr, StatusCode::kInvalidArgument, "null graph");
+    *nodes = static_cast<HipGraphExecutor*>(graph)->node_count();
+  });
+}
+
+int gie_dev_malloc(size_t bytes, void** ptr) {
+  return guarded([&] { GIE_HIP_CHECK(hipMalloc(ptr, bytes)); });
+}
+int gie_dev_free(void* ptr) {
+  return guarded([&] { GIE_HIP_CHECK(hipFree(ptr)); });
+}
+int gie_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return guarded([&] { GIE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice)); });
+}
+int gie_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return guarded([&] { GIE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost)); });
+}
+int gie_memcpy_d2d_async(void* dst, const void* src, size_t bytes, void* stream) {
+  return guarded([&] {
+    GIE_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+  });
+}
+int gie_memset(void* ptr, int value, size_t bytes) {
+  return guarded([&] {
+    GIE_HIP_CHECK(hipMemset(ptr, value, bytes));
+    GIE_HIP_CHECK(hipDeviceSynchronize());
+  });
+}
+int gie_device_synchronize(void) {
+  return guarded([&] { GIE_HIP_CHECK(hipDeviceSynchronize()); });
+}
+int gie_get_device_count(int* n) {
+  return guarded([&] { GIE_HIP_CHECK(hipGetDeviceCount(n)); });
+}
+int gie_set_device(int device) {
+  return guarded([&] { GIE_HIP_CHECK(hipSetDevice(device)); });
+}
+int gie_stream_create(void** stream) {
+  return guarded([&] {
+    hipStream_t s;
+    GIE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+  });
+}
+int gie_stream_destroy(void* stream) {
+  return guarded([&] { GIE_HIP_CHECK(hipStreamDestroy(static_cast<hipStream_t>(stream))); });
+}
+int gie_stream_synchronize(void* stream) {
+  return guarded([&] { GIE_HIP_CHECK(hipStreamSynchronize(static_cast<hipStream_t>(stream))); });
+}
+int gie_event_create(void** ev) {
+  return guarded([&] {
+    hipEvent_t e;
+    GIE_HIP_CHECK(hipEventCreate(&e));
+    *ev = e;
+  });
+}
+int gie_event_destroy(void* ev) {
+  return guarded([&] { GIE_HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(ev))); });
+}
+int gie_event_record(void* ev, void* stream) {
+  return guarded([&] { GIE_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev), static_cast<hipStream_t>(stream))); });
+}
+int gie_event_synchronize(void* ev) {
+  return guarded([&] { GIE_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(ev))); });
+}
+int gie_event_elapsed_ms(void* start, void* stop, float* ms) {
+  return guarded([&] {
+    GIE_HIP_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Microbenchmarks behind the cost model's measured ceilings (the role of src/profiling/ceilings.cu:21-58):
+// a matrix-core loop (4 independent 16x16x32 f16 MFMA chains per wave, operands in registers), a 16-byte
+// vector copy for HBM bandwidth, and an empty kernel for launch cost. Each is a single launch timed by the caller.
+#include "device_common.h"
+
+namespace gie_hip {
+namespace {
+
+__global__ __launch_bounds__(256) void mfma_loop_kernel(int iters, float* __restrict__ sink) {
+  const uint32_t t = threadIdx.x;
+  u32x4 a = {t * 0x3c003c00u, t, t ^ 0x1234u, 0x3c00u};
+  u32x4 b = {0x3c003c00u, t + 1u, 0x3800u, t};
+  f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+  for (int i = 0; i < iters; ++i) {
+    c0 = Fp16::mfma(a, b, c0);
+    c1 = Fp16::mfma(b, a, c1);
+    c2 = Fp16::mfma(a, a, c2);
+    c3 = Fp16::mfma(b, b, c3);
+  }
+  const float v = c0[0] + c1[1] + c2[2] + c3[3];
+  if (v == 1234.5f) sink[blockIdx.x] = v;  // practically never true; keeps the loop alive
+}
+
+__global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst, long long n) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x)
+    dst[i] = src[i];
+}
+
+__global__ void empty_kernel() {}
+
+int launched() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GIE_HIP_OK : int(e);
+}
+
+}  // namespace
+}  // namespace gie_hip
+
+using namespace gie_hip;
+
+extern "C" int gie_hip_ceiling_mfma(int blocks, int iters, float* sink, void* stream) {
+  if (blocks <= 0 || iters <= 0 || !sink) return GIE_HIP_EINVAL;
+  hipLaunchKernelGGL(mfma_loop_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), iters, sink);
+  return launched();
+}
+
+extern "C" int gie_hip_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream) {
+  if (!src || !dst || bytes == 0 || bytes % 16 != 0) return GIE_HIP_EINVAL;
+  const long long n = static_cast<long long>(bytes / 16);
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  long long blocks = (n + 255) / 256;
+  if (blocks > static_cast<long long>(cus) * 16) blocks = static_cast<long long>(cus) * 16;
+  hipLaunchKernelGGL(copy_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), n);
+  return launched();
+}
+
+extern "C" int gie_hip_ceiling_empty(void* stream) {
+  hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream));
+  return launched();
+}

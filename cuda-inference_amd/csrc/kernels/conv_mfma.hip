@@ -1,0 +1,375 @@
+// Implicit-GEMM convolution on gfx950 matrix cores (v_mfma_f32_16x16x32_{f16,bf16}), FP32 accumulation.
+//
+// GEMM view (reference naming): M = out_channels, N = batch*out_h*out_w output pixels, K = kh*kw*c_pad with k
+// ordered (r, s, c) so 8 consecutive k are 8 consecutive channels of one input pixel in the NHWC repack — one
+// 16-byte vector. Inside the kernel the MFMA "row" operand is the activation tile (pixels) and the "column"
+// operand the weight tile (output channels): the 16x16 accumulator then gives each lane 4 consecutive output
+// pixels of one output channel, which are contiguous in NCHW and leave as one 8-byte store.
+//
+// Workgroup: WP x WC wave64s own a TP(pixels) x TC(channels) output tile and walk K in BK slices.
+//   * global -> registers: each thread owns fixed tile rows and one 16-byte K chunk column; activation rows
+//     gather from the NHWC buffer at the (r, s) tap of that chunk (zero outside the image / past K), weight
+//     rows are contiguous along K. The tap cursor advances incrementally (no per-slice division or LUT).
+//   * registers -> LDS: two stages, rows padded by 16 bytes so the 16-lane ds_read_b128 fragment reads of an
+//     MFMA operand hit distinct banks.
+//   * the next slice's global loads are issued before the current slice's MFMAs, so HBM/L2 latency hides
+//     behind matrix work; one barrier per slice.
+//   * epilogue: bias + ReLU on the FP32 accumulators, one RNE rounding, NCHW store (split == 1); or FP32
+//     partials for split-K, summed by splitk_reduce.hip.
+// Split-K slices follow the reference's partition rule [floor(kt*z/S), floor(kt*(z+1)/S))
+// (src/kernels/tensor_core_mma.cu:112-115) and its partial layout partial[z][NCHW] (:231-234).
+#include <mutex>
+#include <set>
+#include <utility>
+#include <vector>
+
+#include "device_common.h"
+
+namespace gie_hip {
+namespace {
+
+struct Geom {
+  int B, C, H, W, O, KH, KW, SH, SW, PH, PW, OH, OW, Cp, relu;
+  int HWo;      // OH * OW
+  int N;        // B * HWo output pixels
+  int Kp;       // KH * KW * Cp
+  int img;      // H * W * Cp elements per repacked image
+};
+
+template <int TP, int TC, int BK, int WP, int WC>
+struct Shape {
+  static constexpr int NT = WP * WC * 64;
+  static constexpr int WTP = TP / WP, WTC = TC / WC;  // per-wave tile
+  static constexpr int FP = WTP / 16, FC = WTC / 16;  // 16x16 MFMA blocks per wave
+  static constexpr int LDK = BK + 8;                  // LDS row pitch in 16-bit elements
+  static constexpr int CPR = BK / 8;                  // 16-byte chunks per tile row
+  static constexpr int LA = TP * CPR / NT, LB = TC * CPR / NT;
+  static constexpr int kLds = 2 * (TP + TC) * LDK * 2;
+  static_assert(TP % (WP * 16) == 0 && TC % (WC * 16) == 0, "wave tile must be a multiple of 16x16");
+  static_assert(BK % 32 == 0, "BK must be a multiple of the MFMA K (32)");
+  static_assert((TP * CPR) % NT == 0 && (TC * CPR) % NT == 0 && NT % CPR == 0, "chunks must divide over threads");
+};
+
+template <typename E, int TP, int TC, int BK, int WP, int WC>
+__global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __restrict__ xn,
+                                                             const uint16_t* __restrict__ wk,
+                                                             const uint16_t* __restrict__ bias,
+                                                             uint16_t* __restrict__ y, float* __restrict__ partial,
+                                                             Geom g, int split) {
+  using S = Shape<TP, TC, BK, WP, WC>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  uint16_t* sA = reinterpret_cast<uint16_t*>(lds_raw);  // [2][TP][LDK] activations
+  uint16_t* sB = sA + 2 * TP * S::LDK;                  // [2][TC][LDK] weights
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wp = wave / WC, wc = wave % WC;
+  const int n0 = blockIdx.x * TP, m0 = blockIdx.y * TC;
+
+  const int ktiles = (g.Kp + BK - 1) / BK;
+  const int kt_begin = int((static_cast<long long>(ktiles) * blockIdx.z) / split);
+  const int kt_end = int((static_cast<long long>(ktiles) * (blockIdx.z + 1)) / split);
+  const int nk = kt_end - kt_begin;
+  const int kchunks = g.Kp >> 3;
+  const int kc = tid % S::CPR;
+
+  // Fixed rows of this thread: pixel origin of each activation row, base of each weight row.
+  const uint16_t* a_img[S::LA];
+  int a_hb[S::LA], a_wb[S::LA];
+#pragma unroll
+  for (int i = 0; i < S::LA; ++i) {
+    const int n = n0 + (tid + i * S::NT) / S::CPR;
+    if (n < g.N) {
+      const int b = n / g.HWo;
+      const int p = n - b * g.HWo;
+      const int oh = p / g.OW, ow = p - (p / g.OW) * g.OW;
+      a_img[i] = xn + static_cast<long long>(b) * g.img;
+      a_hb[i] = oh * g.SH - g.PH;
+      a_wb[i] = ow * g.SW - g.PW;
+    } else {
+      a_img[i] = xn;
+      a_hb[i] = -0x40000000;  // every tap lands outside the image -> zero row
+      a_wb[i] = 0;
+    }
+  }
+  const uint16_t* b_row[S::LB];
+  bool b_ok[S::LB];
+#pragma unroll
+  for (int i = 0; i < S::LB; ++i) {
+    const int o = m0 + (tid + i * S::NT) / S::CPR;
+    b_ok[i] = o < g.O;
+    b_row[i] = wk + static_cast<long long>(b_ok[i] ? o : 0) * g.Kp;
+  }
+
+  // K cursor of this thread's chunk column: chunk q -> tap (r, s), channel offset c0.
+  int q = kt_begin * S::CPR + kc;
+  const int cvec = g.Cp >> 3;
+  int rs = q / cvec;
+  int c0 = (q - rs * cvec) * 8;
+  int r = rs / g.KW;
+  int s = rs - r * g.KW;
+
+  u32x4 ra[S::LA], rb[S::LB];
+  auto gload = [&]() {
+    const bool kok = q < kchunks;
+#pragma unroll
+    for (int i = 0; i < S::LA; ++i) {
+      const int ih = a_hb[i] + r, iw = a_wb[i] + s;
+      const bool ok = kok && ih >= 0 && ih < g.H && iw >= 0 && iw < g.W;
+      ra[i] = ok ? *reinterpret_cast<const u32x4*>(a_img[i] + (ih * g.W + iw) * g.Cp + c0) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < S::LB; ++i) {
+      const bool ok = kok && b_ok[i];
+      rb[i] = ok ? *reinterpret_cast<const u32x4*>(b_row[i] + q * 8) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto advance = [&]() {
+    q += S::CPR;
+    c0 += BK;
+    while (c0 >= g.Cp) {
+      c0 -= g.Cp;
+      if (++s == g.KW) {
+        s = 0;
+        ++r;
+      }
+    }
+  };
+  auto sstore = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < S::LA; ++i) {
+      const int row = (tid + i * S::NT) / S::CPR;
+      *reinterpret_cast<u32x4*>(sA + (st * TP + row) * S::LDK + kc * 8) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < S::LB; ++i) {
+      const int row = (tid + i * S::NT) / S::CPR;
+      *reinterpret_cast<u32x4*>(sB + (st * TC + row) * S::LDK + kc * 8) = rb[i];
+    }
+  };
+
+  f32x4 acc[S::FP][S::FC];
+#pragma unroll
+  for (int i = 0; i < S::FP; ++i)
+#pragma unroll
+    for (int j = 0; j < S::FC; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (nk > 0) {
+    gload();
+    advance();
+    sstore(0);
+  }
+  __syncthreads();
+
+  const int frag_row = lane & 15, frag_k = (lane >> 4) * 8;
+  for (int it = 0; it < nk; ++it) {
+    const int st = it & 1;
+    const bool more = it + 1 < nk;
+    if (more) {
+      gload();
+      advance();
+    }
+    const uint16_t* tA = sA + (st * TP + wp * S::WTP + frag_row) * S::LDK + frag_k;
+    const uint16_t* tB = sB + (st * TC + wc * S::WTC + frag_row) * S::LDK + frag_k;
+#pragma unroll
+    for (int kk = 0; kk < BK / 32; ++kk) {
+      u32x4 af[S::FP], bf[S::FC];
+#pragma unroll
+      for (int i = 0; i < S::FP; ++i) af[i] = *reinterpret_cast<const u32x4*>(tA + i * 16 * S::LDK + kk * 32);
+#pragma unroll
+      for (int j = 0; j < S::FC; ++j) bf[j] = *reinterpret_cast<const u32x4*>(tB + j * 16 * S::LDK + kk * 32);
+#pragma unroll
+      for (int i = 0; i < S::FP; ++i)
+#pragma unroll
+        for (int j = 0; j < S::FC; ++j) acc[i][j] = E::mfma(af[i], bf[j], acc[i][j]);
+    }
+    if (more) sstore(st ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue. Lane holds, for MFMA block (i, j), pixels nb..nb+3 of output channel o.
+  const long long total = static_cast<long long>(g.N) * g.O;
+#pragma unroll
+  for (int i = 0; i < S::FP; ++i) {
+    const int nb = n0 + wp * S::WTP + i * 16 + (lane >> 4) * 4;
+    if (nb >= g.N) continue;
+    const int b = nb / g.HWo;
+    const int p = nb - b * g.HWo;
+    const bool whole = nb + 3 < g.N && p + 3 < g.HWo;  // 4 pixels, same image
+#pragma unroll
+    for (int j = 0; j < S::FC; ++j) {
+      const int o = m0 + wc * S::WTC + j * 16 + (lane & 15);
+      if (o >= g.O) continue;
+      const f32x4 v = acc[i][j];
+      const long long idx = (static_cast<long long>(b) * g.O + o) * g.HWo + p;
+      if (split > 1) {
+        float* pz = partial + blockIdx.z * total;
+        if (whole && (reinterpret_cast<uintptr_t>(pz + idx) & 15u) == 0) {
+          *reinterpret_cast<f32x4*>(pz + idx) = v;
+        } else {
+          for (int e = 0; e < 4; ++e) {
+            const int n = nb + e;
+            if (n >= g.N) break;
+            const int be = n / g.HWo, pe = n - be * g.HWo;
+            pz[(static_cast<long long>(be) * g.O + o) * g.HWo + pe] = v[e];
+          }
+        }
+      } else {
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = epilogue<E>(v[e], bias, o, g.relu);
+        uint16_t* dst = y + idx;
+        if (whole && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{uint32_t(h[0]) | (uint32_t(h[1]) << 16),
+                                                 uint32_t(h[2]) | (uint32_t(h[3]) << 16)};
+        } else {
+          for (int e = 0; e < 4; ++e) {
+            const int n = nb + e;
+            if (n >= g.N) break;
+            const int be = n / g.HWo, pe = n - be * g.HWo;
+            y[(static_cast<long long>(be) * g.O + o) * g.HWo + pe] = h[e];
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---- registered configurations --------------------------------------------------------------------------------
+typedef void (*KernelFn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, Geom, int);
+
+struct Config {
+  gie_igemm_config info;
+  KernelFn fp16, bf16;
+};
+
+template <int TP, int TC, int BK, int WP, int WC>
+Config make_config(int version) {
+  using S = Shape<TP, TC, BK, WP, WC>;
+  Config c;
+  // reference naming: M = out channels (TC here), N = pixels (TP here)
+  c.info.tile_m = TC;
+  c.info.tile_n = TP;
+  c.info.tile_k = BK;
+  c.info.waves_m = WC;
+  c.info.waves_n = WP;
+  c.info.threads = S::NT;
+  c.info.lds_bytes = S::kLds;
+  c.info.version = version;
+  c.fp16 = &igemm_kernel<Fp16, TP, TC, BK, WP, WC>;
+  c.bf16 = &igemm_kernel<Bf16, TP, TC, BK, WP, WC>;
+  return c;
+}
+
+const std::vector<Config>& configs() {
+  static const std::vector<Config> table = [] {
+    std::vector<Config> t;
+    //            pixels x channels x k, waves (pixels x channels)
+    t.push_back(make_config<128, 128, 32, 2, 2>(1));
+    t.push_back(make_config<128, 128, 64, 2, 2>(1));
+    t.push_back(make_config<128, 64, 32, 2, 2>(1));
+    t.push_back(make_config<128, 64, 64, 2, 2>(1));
+    t.push_back(make_config<64, 128, 32, 2, 2>(1));
+    t.push_back(make_config<64, 128, 64, 2, 2>(1));
+    t.push_back(make_config<64, 64, 32, 2, 2>(1));
+    t.push_back(make_config<64, 64, 64, 2, 2>(1));
+    t.push_back(make_config<256, 128, 32, 4, 2>(1));
+    t.push_back(make_config<128, 256, 32, 2, 4>(1));
+    t.push_back(make_config<32, 64, 64, 1, 2>(1));
+    return t;
+  }();
+  return table;
+}
+
+int set_lds_limit(KernelFn fn, int bytes) {
+  if (bytes <= 64 * 1024) return GIE_HIP_OK;
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return int(hipErrorInvalidDevice);
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({reinterpret_cast<const void*>(fn), dev})) return GIE_HIP_OK;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return int(e);
+  done.insert({reinterpret_cast<const void*>(fn), dev});
+  return GIE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace gie_hip
+
+using namespace gie_hip;
+
+extern "C" int gie_hip_igemm_config_count(void) { return int(configs().size()); }
+
+extern "C" int gie_hip_igemm_config_get(int index, gie_igemm_config* out) {
+  if (index < 0 || index >= int(configs().size()) || !out) return GIE_HIP_EINVAL;
+  *out = configs()[size_t(index)].info;
+  return GIE_HIP_OK;
+}
+
+extern "C" int gie_hip_igemm_occupancy(int index, int dtype, int* blocks_per_cu) {
+  if (index < 0 || index >= int(configs().size()) || !blocks_per_cu) return GIE_HIP_EINVAL;
+  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
+  const Config& c = configs()[size_t(index)];
+  KernelFn fn = dtype == GIE_HIP_FP16 ? c.fp16 : c.bf16;
+  if (int rc = set_lds_limit(fn, c.info.lds_bytes)) return rc;
+  int n = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn),
+                                                                     c.info.threads, size_t(c.info.lds_bytes));
+  if (e != hipSuccess) return int(e);
+  *blocks_per_cu = n;
+  return GIE_HIP_OK;
+}
+
+extern "C" int gie_hip_conv_igemm(int config, int dtype, const gie_conv_geom* gg, const void* xn, const void* wk,
+                                  const void* bias, void* y, float* partial, int split, void* stream) {
+  if (config < 0 || config >= int(configs().size()) || !gg || !xn || !wk) return GIE_HIP_EINVAL;
+  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
+  if (split < 1 || split > 64) return GIE_HIP_EINVAL;
+  if (split == 1 && !y) return GIE_HIP_EINVAL;
+  if (split > 1 && (!partial || (reinterpret_cast<uintptr_t>(partial) & 15u) != 0)) return GIE_HIP_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(xn) & 15u) != 0 || (reinterpret_cast<uintptr_t>(wk) & 15u) != 0)
+    return GIE_HIP_EINVAL;
+  const Config& c = configs()[size_t(config)];
+  Geom g;
+  g.B = gg->batch;
+  g.C = gg->in_channels;
+  g.H = gg->in_h;
+  g.W = gg->in_w;
+  g.O = gg->out_channels;
+  g.KH = gg->kernel_h;
+  g.KW = gg->kernel_w;
+  g.SH = gg->stride_h;
+  g.SW = gg->stride_w;
+  g.PH = gg->pad_h;
+  g.PW = gg->pad_w;
+  g.OH = gg->out_h;
+  g.OW = gg->out_w;
+  g.Cp = gg->c_pad;
+  g.relu = gg->relu ? 1 : 0;
+  if (g.B <= 0 || g.C <= 0 || g.H <= 0 || g.W <= 0 || g.O <= 0 || g.KH <= 0 || g.KW <= 0 || g.SH <= 0 || g.SW <= 0 ||
+      g.PH < 0 || g.PW < 0 || g.OH <= 0 || g.OW <= 0 || g.Cp < g.C || (g.Cp & 7) != 0)
+    return GIE_HIP_EINVAL;
+  // every index the kernel forms in 32 bits must fit
+  const long long hwo = static_cast<long long>(g.OH) * g.OW;
+  const long long n = hwo * g.B;
+  const long long kp = static_cast<long long>(g.KH) * g.KW * g.Cp;
+  const long long img = static_cast<long long>(g.H) * g.W * g.Cp;
+  if (n > 0x7fffffffLL || kp > 0x7fffffffLL || img > 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
+  g.HWo = int(hwo);
+  g.N = int(n);
+  g.Kp = int(kp);
+  g.img = int(img);
+  const long long gx = (n + c.info.tile_n - 1) / c.info.tile_n;
+  const long long gy = (g.O + c.info.tile_m - 1) / c.info.tile_m;
+  if (gx > 0x7fffffffLL || gy > 65535) return GIE_HIP_EUNSUPPORTED;
+  KernelFn fn = dtype == GIE_HIP_FP16 ? c.fp16 : c.bf16;
+  if (int rc = set_lds_limit(fn, c.info.lds_bytes)) return rc;
+  hipLaunchKernelGGL(fn, dim3(unsigned(gx), unsigned(gy), unsigned(split)), dim3(c.info.threads), c.info.lds_bytes,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(xn),
+                     static_cast<const uint16_t*>(wk), static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+                     partial, g, split);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GIE_HIP_OK : int(e);
+}

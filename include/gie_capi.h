@@ -1,0 +1,165 @@
+/* C-ABI over the gie:: C++ plan API (libgie.so), for hosts that bind C rather than C++ (ctypes, cgo, JNI).
+ *
+ * The reference exposes this path only as C++ (the gpu_inference headers); each function below is a flat
+ * wrapper over one of those calls and cites it (paths relative to the reference checkout). Exceptions never
+ * cross this boundary: every function returns 0 or a gie::StatusCode value
+ * (1 InvalidArgument, 2 Unsupported, 3 WorkspaceTooSmall, 4 HipError, 5 Internal, 6 Io) and leaves the
+ * message in gie_last_error() (thread-local). Streams/events/plans/graphs are opaque `void*` handles.
+ */
+#ifndef GIE_CAPI_H_
+#define GIE_CAPI_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ConvProblem (include/gpu_inference/conv2d.h:47-85). precision: 0 fp32, 1 fp16, 2 bf16, 3 tf32 */
+typedef struct gie_problem {
+  int batch, in_channels, in_h, in_w, out_channels, kernel_h, kernel_w;
+  int stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups;
+  int precision, has_bias, relu;
+} gie_problem;
+
+/* Conv2DOptions (conv2d.h:90-96). backend: 0 auto, 1 cpu_reference, 2 direct, 3 im2col_gemm, 4 simt_tiled,
+   5 implicit_gemm, 6 tensor_core. kernel / cache_path may be null. */
+typedef struct gie_options {
+  int backend;
+  const char* kernel;
+  int autotune, force_retune;
+  const char* cache_path;
+} gie_options;
+
+/* A tensor view (ConstTensorRef / TensorRef, tensor.h:45-66). dtype: 0 float32, 1 float16, 2 bfloat16 */
+typedef struct gie_tensor {
+  const void* data;
+  int dtype;
+  int64_t n, c, h, w;
+} gie_tensor;
+
+const char* gie_last_error(void);
+const char* gie_status_string(int status);
+
+/* ---- problem ---- */
+int gie_validate_problem(const gie_problem* p);                              /* conv2d.cpp:83-109 */
+int gie_problem_key(const gie_problem* p, char* buf, size_t n);              /* conv2d.cpp:77-81 */
+
+/* ---- Conv2D (conv2d.h:98-112) ---- */
+int gie_conv2d_forward(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                       const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
+                       const gie_options* opt);
+/* `count` back-to-back Conv2D::forward calls on one stream (plan lookup + argument validation + launch each
+   time): the benchmark's timed step without a host-language loop in the way */
+int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                         const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
+                         const gie_options* opt, int count);
+int gie_conv2d_workspace_size(const gie_problem* p, const gie_options* opt, size_t* bytes);
+int gie_conv2d_clear_plan_cache(void);
+
+/* ---- ExecutionPlan (execution_plan.h:14-51) ---- */
+int gie_plan_create(const gie_problem* p, const char* kernel_name, int device, void** plan);
+int gie_plan_destroy(void* plan);
+int gie_plan_workspace_bytes(void* plan, size_t* bytes);
+int gie_plan_kernel_name(void* plan, char* buf, size_t n);
+int gie_plan_execute(void* plan, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                     const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream);
+int gie_plan_execute_unchecked(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                               size_t workspace_bytes, void* stream);
+/* time_stream_work (timing.h:36-38) around execute_unchecked; stats = {median, mean, min, max, p10, p90, stddev}
+   in microseconds per call, *inner = launches per sample */
+int gie_plan_time(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                  size_t workspace_bytes, void* stream, int warmup, int samples, double min_sample_ms,
+                  double* stats7, int* inner);
+/* per-stage device time of one call, averaged over `iters` calls bracketed by stage events:
+   us3 = {repack, implicit GEMM, split-K reduce (0 when split == 1)} */
+int gie_plan_time_stages(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                         size_t workspace_bytes, void* stream, int iters, double* us3);
+
+/* ---- registry / dispatcher (kernel_registry.h:76-82, dispatcher.h:34-53) ---- */
+int gie_registry_count(void);
+int gie_registry_name(int index, char* buf, size_t n);
+/* params as "key=value,key=value" and flags */
+int gie_kernel_describe(const char* name, char* buf, size_t n);
+int gie_kernel_supports(const char* name, const gie_problem* p, int* ok, char* why, size_t why_n);
+/* source: 0 forced_kernel, 1 forced_backend, 2 tuning_cache, 3 tuned, 4 cost_model */
+int gie_dispatch_select(const gie_problem* p, const gie_options* opt, char* kernel, size_t n, int* source,
+                        double* predicted_us);
+/* cost-model ranking of all compatible kernels: names joined by '\n' into buf, predicted us into us[max] */
+int gie_rank_by_model(const gie_problem* p, char* buf, size_t n, double* us, int max, int* count);
+
+/* ---- autotuner / tune cache (autotuner.h:21-93) ---- */
+typedef struct gie_tune_options {
+  int warmup, samples;
+  double min_sample_ms;
+  uint64_t seed;
+  int validate, model_keep, max_candidates, use_cache, force_retune, verbose;
+  const char* cache_path;
+} gie_tune_options;
+void gie_tune_options_default(gie_tune_options* o);
+/* best kernel name into best; counts: {candidates_total, candidates_measured, from_cache, n_rejected,
+   n_failed_validation, n_error} */
+int gie_autotune(const gie_problem* p, const gie_tune_options* o, char* best, size_t n, double* best_us,
+                 double* search_seconds, int* counts6);
+int gie_tune_cache_key(const gie_problem* p, int scope_backend, char* buf, size_t n);
+int gie_tune_cache_size(const char* path, size_t* size);
+int gie_tune_cache_clear(const char* path);
+
+/* ---- cost model (perf_model.h) ---- */
+/* out6 = {time_us, compute_us, memory_us, launch_us, tile_efficiency, wave_efficiency}; bound: 0/1/2 */
+int gie_estimate_kernel(const char* name, const gie_problem* p, double* out6, int* bound);
+/* out3 = {fp16_mfma_tflops, bw_gbs, launch_overhead_us} */
+int gie_measure_ceilings(int device, int use_cache, double* out3, int* measured);
+int gie_theoretical_ceilings(int device, double* out3);
+
+/* ---- reference and device description ---- */
+/* GPU double reference (reference.h:36-39): y, scale float device buffers */
+int gie_gpu_reference(const gie_problem* p, const void* x, const void* w, const void* bias, float* y, float* scale,
+                      void* stream);
+/* CPU reference of the library (reference.h:31-34) on host float arrays */
+int gie_cpu_reference(const gie_problem* p, const float* x, const float* w, const float* bias, float* y,
+                      float* scale);
+/* make_conv_data's host half (testing.h): seeded draws x, w, bias quantized to the storage type.
+   dist: 0 uniform, 1 normal, 2 sparse_signed, 3 positive; scaling: 0 reference, 1 benchmark */
+int gie_make_host_data(const gie_problem* p, uint64_t seed, int dist, int scaling, float* x, float* w, float* bias);
+int gie_device_describe(int device, char* buf, size_t n);
+int gie_device_arch(int device, char* buf, size_t n);
+int gie_device_cu_count(int device, int* cus);
+int gie_build_fingerprint(char* buf, size_t n);
+
+/* ---- HipGraphExecutor (cuda_graph.h:14-46) over a chain of plan executions ---- */
+int gie_graph_create(void** graph);
+int gie_graph_destroy(void* graph);
+/* captures plans[i]->execute_unchecked(xs[i], ws[i], biases[i], ys[i], wss[i], ws_bytes[i]) for i = 0..n-1 */
+int gie_graph_capture_chain(void* graph, int n, void* const* plans, const void* const* xs, const void* const* ws,
+                            const void* const* biases, void* const* ys, void* const* wss, const size_t* ws_bytes);
+int gie_graph_recapture_chain(void* graph, int n, void* const* plans, const void* const* xs, const void* const* ws,
+                              const void* const* biases, void* const* ys, void* const* wss, const size_t* ws_bytes,
+                              int* updated_in_place);
+int gie_graph_launch(void* graph, void* stream);
+int gie_graph_node_count(void* graph, size_t* nodes);
+
+/* ---- device memory / streams / events for bindings without their own HIP runtime ---- */
+int gie_dev_malloc(size_t bytes, void** ptr);
+int gie_dev_free(void* ptr);
+int gie_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int gie_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int gie_memcpy_d2d_async(void* dst, const void* src, size_t bytes, void* stream);
+int gie_memset(void* ptr, int value, size_t bytes);
+int gie_device_synchronize(void);
+int gie_get_device_count(int* n);
+int gie_set_device(int device);
+int gie_stream_create(void** stream);
+int gie_stream_destroy(void* stream);
+int gie_stream_synchronize(void* stream);
+int gie_event_create(void** ev);
+int gie_event_destroy(void* ev);
+int gie_event_record(void* ev, void* stream);
+int gie_event_synchronize(void* ev);
+int gie_event_elapsed_ms(void* start, void* stop, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,107 @@
+/* C-ABI of the MI355X (gfx950) Conv2D kernels — the drop-in boundary under the gie:: C++ plan API.
+ *
+ * The C++ runtime (KernelDesc::launch implementations) calls only these functions. Every entry point takes
+ * plain device pointers, sizes and a hipStream_t passed as `void*`; none allocates, frees or synchronizes,
+ * so a sequence of calls can be captured into a hipGraph. Exceptions never cross this boundary: each call
+ * returns 0 on success, a negative GIE_HIP_E* code for a rejected argument, or a positive hipError_t from
+ * the launch (the host wrapper turns both into gie::Error).
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   gie_hip_repack_act_nchw_to_nhwc  launch_transpose(x, xn, B, C, H*W)    src/kernels/tensor_core_mma.cu:78-82,309
+ *   gie_hip_repack_w_oihw_to_orsc    launch_transpose(w, wk, O, C, KH*KW)  src/kernels/tensor_core_mma.cu:78-82,310
+ *   gie_hip_conv_igemm               tcmma_kernel<<<>>> launch             src/kernels/tensor_core_mma.cu:99-251,311-316
+ *   gie_hip_splitk_reduce            splitk_reduce<<<>>> launch            src/kernels/tensor_core_mma.cu:254-262,317-323
+ *   gie_hip_igemm_config_*           the registered tile table             src/kernels/tensor_core_mma.cu:370-388
+ *   gie_hip_igemm_occupancy          cudaOccupancyMaxActiveBlocksPerMultiprocessor in src/runtime/perf_model.cpp:75-102
+ *   gie_hip_reference_conv           gpu_conv2d_reference                  src/runtime/reference.cu:31-91
+ *   gie_hip_ceiling_*                ceilings microbenchmarks              src/profiling/ceilings.cu:21-58
+ */
+#ifndef GIE_HIP_H_
+#define GIE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes (0 = ok, > 0 = hipError_t) */
+#define GIE_HIP_OK 0
+#define GIE_HIP_EINVAL (-1)      /* null pointer, bad size, shape the kernel's grid cannot cover */
+#define GIE_HIP_EUNSUPPORTED (-2) /* valid request this kernel configuration cannot run */
+
+/* element types; numbering follows gie::Precision (kFp32 = 0, kFp16 = 1, kBf16 = 2) */
+#define GIE_HIP_FP32 0
+#define GIE_HIP_FP16 1
+#define GIE_HIP_BF16 2
+
+/* Convolution geometry as the kernels see it (dilation and groups are 1, enforced by the host). */
+typedef struct gie_conv_geom {
+  int batch, in_channels, in_h, in_w;
+  int out_channels, kernel_h, kernel_w;
+  int stride_h, stride_w, pad_h, pad_w;
+  int out_h, out_w;
+  int c_pad; /* channel count of the repacked activation / weight buffers: multiple of 8, >= in_channels */
+  int relu;  /* 1: ReLU after bias */
+} gie_conv_geom;
+
+/* One registered implicit-GEMM tile configuration. GEMM view as the reference names it:
+   M = out_channels (tile_m), N = batch*out_h*out_w pixels (tile_n), K = kernel_h*kernel_w*c_pad (tile_k). */
+typedef struct gie_igemm_config {
+  int tile_m, tile_n, tile_k;
+  int waves_m, waves_n; /* wave64 grid inside a workgroup */
+  int threads;          /* waves_m * waves_n * 64 */
+  int lds_bytes;        /* LDS per workgroup (two stages of the A and B tiles) */
+  int version;          /* bumps when the kernel's code changes behaviour or speed */
+} gie_igemm_config;
+
+const char* gie_hip_status_string(int status);
+
+/* x: [batch][channels][hw] 16-bit elements (any 2-byte alignment); xn: [batch][hw][c_pad], 16-byte aligned.
+   xn[b][p][c] = x[b][c][p] for c < channels, 0 for channels <= c < c_pad. Bit-exact permutation. */
+int gie_hip_repack_act_nchw_to_nhwc(const void* x, void* xn, int batch, int channels, int hw, int c_pad,
+                                    void* stream);
+
+/* w: [out_channels][channels][rs] (OIHW) -> wk: [out_channels][rs][c_pad], zero channel padding. */
+int gie_hip_repack_w_oihw_to_orsc(const void* w, void* wk, int out_channels, int channels, int rs, int c_pad,
+                                  void* stream);
+
+/* The two repacks above in one launch (same results; one dispatch instead of two). */
+int gie_hip_repack_act_and_w(const void* x, void* xn, const void* w, void* wk, const gie_conv_geom* g,
+                             void* stream);
+
+int gie_hip_igemm_config_count(void);
+int gie_hip_igemm_config_get(int index, gie_igemm_config* out);
+/* resident workgroups per CU for that configuration and element type */
+int gie_hip_igemm_occupancy(int index, int dtype, int* blocks_per_cu);
+
+/* Implicit-GEMM convolution on MFMA (FP16/BF16 storage, FP32 accumulation) over the repacked buffers.
+   split == 1: y (NCHW, dtype, any 2-byte alignment) = round(relu?(acc + bias)) — one rounding.
+   split  > 1: partial[z][NCHW index] = FP32 sum over the z-th slice of the K tiles
+               [floor(kt*z/split), floor(kt*(z+1)/split)); y and bias are not touched (reduce below).
+   bias may be null. partial must be 16-byte aligned and hold split*batch*out_channels*out_h*out_w floats. */
+int gie_hip_conv_igemm(int config, int dtype, const gie_conv_geom* g, const void* xn, const void* wk,
+                       const void* bias, void* y, float* partial, int split, void* stream);
+
+/* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels])) */
+int gie_hip_splitk_reduce(int dtype, const float* partial, const void* bias, void* y, int64_t total, int split,
+                          int out_channels, int hw_out, int relu, void* stream);
+
+/* Double-accumulation direct convolution (validation reference for the autotuner and tests):
+   y_ref, scale: float[batch*out_channels*out_h*out_w]. dtype may be GIE_HIP_FP32 here. */
+int gie_hip_reference_conv(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias,
+                           float* y_ref, float* scale, void* stream);
+
+/* Ceiling microbenchmarks (one launch each; the caller times them with events).
+   mfma: `blocks` workgroups of 256 threads issuing `iters` dependent-free 16x16x32 f16 MFMAs per wave
+   (flops = blocks * 4 waves * iters * 4 chains * 16384); copy: dst = src, `bytes` multiple of 16;
+   empty: one 64-thread workgroup that does nothing. `sink` receives a value so nothing is optimized out. */
+int gie_hip_ceiling_mfma(int blocks, int iters, float* sink, void* stream);
+int gie_hip_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream);
+int gie_hip_ceiling_empty(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
