@@ -1,6 +1,7 @@
 // Flat C-ABI over the gie:: C++ API (include/gie_capi.h). Each function catches every exception and turns it
 // into a status code plus a thread-local message.
 #include "gie_capi.h"
+#include "gie_hip.h"
 
 #include <hip/hip_runtime.h>
 
@@ -598,3 +599,46 @@ int gie_event_elapsed_ms(void* start, void* stop, float* ms) {
 }
 
 }  // extern "C"
+
+// ---- testing hook: faulty registry entries (kernel_registry_for_testing) ----
+namespace {
+bool faulty_supports_fp16(const ConvProblem& p, const DeviceInfo&, std::string* why) {
+  if (p.precision == Precision::kFp16) return true;
+  if (why) *why = "test kernel is fp16 only";
+  return false;
+}
+bool faulty_supports_bf16(const ConvProblem& p, const DeviceInfo&, std::string* why) {
+  if (p.precision == Precision::kBf16) return true;
+  if (why) *why = "test kernel is bf16 only";
+  return false;
+}
+size_t no_workspace(const ConvProblem&) { return 0; }
+void garbage_launch(const LaunchArgs& la) {
+  check_kernel_status(gie_hip_fill_u16(la.y, la.problem->p.output_shape().numel(), 0x3c00, la.stream),
+                      "garbage fill");
+}
+void throwing_launch(const LaunchArgs&) { throw Error(StatusCode::kInternal, "deliberately failing test kernel"); }
+}  // namespace
+
+extern "C" int gie_testing_add_faulty_kernels(int kind) {
+  return guarded([&] {
+    GIE_REQUIRE(kind == 0 || kind == 1, StatusCode::kInvalidArgument, "kind must be 0 (garbage) or 1 (throwing)");
+    std::vector<KernelDesc>& reg = kernel_registry_for_testing();
+    for (Precision p : {Precision::kFp16, Precision::kBf16}) {
+      const std::string name = std::string(kind == 0 ? "test_garbage_" : "test_throwing_") + to_string(p);
+      if (find_kernel(name)) continue;
+      GIE_REQUIRE(reg.size() < reg.capacity(), StatusCode::kInternal, "registry capacity exhausted");
+      KernelDesc k;
+      k.name = name;
+      k.backend = Backend::kTensorCore;
+      k.threads_per_block = 256;
+      k.tile_m = k.tile_n = k.tile_k = 1024;  // a huge tile: the cost model must not be what rejects it
+      k.uses_tensor_cores = true;
+      k.efficiency_prior = 1.0;
+      k.supports = p == Precision::kFp16 ? &faulty_supports_fp16 : &faulty_supports_bf16;
+      k.workspace_bytes = &no_workspace;
+      k.launch = kind == 0 ? &garbage_launch : &throwing_launch;
+      reg.push_back(std::move(k));
+    }
+  });
+}

@@ -29,6 +29,12 @@ __global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src
 
 __global__ void empty_kernel() {}
 
+__global__ __launch_bounds__(256) void fill_u16_kernel(uint16_t* __restrict__ dst, long long n, uint16_t v) {
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * blockDim.x)
+    dst[i] = v;
+}
+
 int launched() {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GIE_HIP_OK : int(e);
@@ -59,5 +65,15 @@ extern "C" int gie_hip_ceiling_copy(const void* src, void* dst, size_t bytes, vo
 
 extern "C" int gie_hip_ceiling_empty(void* stream) {
   hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream));
+  return launched();
+}
+
+extern "C" int gie_hip_fill_u16(void* dst, int64_t n, uint16_t value, void* stream) {
+  if (!dst || n < 0) return GIE_HIP_EINVAL;
+  if (n == 0) return GIE_HIP_OK;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(fill_u16_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint16_t*>(dst), static_cast<long long>(n), value);
   return launched();
 }

@@ -50,7 +50,7 @@ struct Shape {
   static_assert((TP * CPR) % NT == 0 && (TC * CPR) % NT == 0 && NT % CPR == 0, "chunks must divide over threads");
 };
 
-template <typename E, int TP, int TC, int BK, int WP, int WC>
+template <typename E, int TP, int TC, int BK, int WP, int WC, int PF>
 __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __restrict__ xn,
                                                              const uint16_t* __restrict__ wk,
                                                              const uint16_t* __restrict__ bias,
@@ -108,22 +108,21 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
   int r = rs / g.KW;
   int s = rs - r * g.KW;
 
-  u32x4 ra[S::LA], rb[S::LB];
-  auto gload = [&]() {
+  u32x4 ra[PF][S::LA], rb[PF][S::LB];
+  // Loads the slice at the cursor into one register slot, then advances the cursor by one slice.
+  auto gload = [&](u32x4(&A)[S::LA], u32x4(&B)[S::LB]) {
     const bool kok = q < kchunks;
 #pragma unroll
     for (int i = 0; i < S::LA; ++i) {
       const int ih = a_hb[i] + r, iw = a_wb[i] + s;
       const bool ok = kok && ih >= 0 && ih < g.H && iw >= 0 && iw < g.W;
-      ra[i] = ok ? *reinterpret_cast<const u32x4*>(a_img[i] + (ih * g.W + iw) * g.Cp + c0) : u32x4{0, 0, 0, 0};
+      A[i] = ok ? *reinterpret_cast<const u32x4*>(a_img[i] + (ih * g.W + iw) * g.Cp + c0) : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int i = 0; i < S::LB; ++i) {
       const bool ok = kok && b_ok[i];
-      rb[i] = ok ? *reinterpret_cast<const u32x4*>(b_row[i] + q * 8) : u32x4{0, 0, 0, 0};
+      B[i] = ok ? *reinterpret_cast<const u32x4*>(b_row[i] + q * 8) : u32x4{0, 0, 0, 0};
     }
-  };
-  auto advance = [&]() {
     q += S::CPR;
     c0 += BK;
     while (c0 >= g.Cp) {
@@ -134,16 +133,16 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
       }
     }
   };
-  auto sstore = [&](int st) {
+  auto sstore = [&](int st, const u32x4(&A)[S::LA], const u32x4(&B)[S::LB]) {
 #pragma unroll
     for (int i = 0; i < S::LA; ++i) {
       const int row = (tid + i * S::NT) / S::CPR;
-      *reinterpret_cast<u32x4*>(sA + (st * TP + row) * S::LDK + kc * 8) = ra[i];
+      *reinterpret_cast<u32x4*>(sA + (st * TP + row) * S::LDK + kc * 8) = A[i];
     }
 #pragma unroll
     for (int i = 0; i < S::LB; ++i) {
       const int row = (tid + i * S::NT) / S::CPR;
-      *reinterpret_cast<u32x4*>(sB + (st * TC + row) * S::LDK + kc * 8) = rb[i];
+      *reinterpret_cast<u32x4*>(sB + (st * TC + row) * S::LDK + kc * 8) = B[i];
     }
   };
 
@@ -153,21 +152,8 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
 #pragma unroll
     for (int j = 0; j < S::FC; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (nk > 0) {
-    gload();
-    advance();
-    sstore(0);
-  }
-  __syncthreads();
-
   const int frag_row = lane & 15, frag_k = (lane >> 4) * 8;
-  for (int it = 0; it < nk; ++it) {
-    const int st = it & 1;
-    const bool more = it + 1 < nk;
-    if (more) {
-      gload();
-      advance();
-    }
+  auto compute = [&](int st) {
     const uint16_t* tA = sA + (st * TP + wp * S::WTP + frag_row) * S::LDK + frag_k;
     const uint16_t* tB = sB + (st * TC + wc * S::WTC + frag_row) * S::LDK + frag_k;
 #pragma unroll
@@ -182,8 +168,29 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
 #pragma unroll
         for (int j = 0; j < S::FC; ++j) acc[i][j] = E::mfma(af[i], bf[j], acc[i][j]);
     }
-    if (more) sstore(st ^ 1);
-    __syncthreads();
+  };
+
+  // Software pipeline: PF register slots hold the next K slices in flight (slot it % PF holds slice it), LDS
+  // holds the slice being multiplied. Iteration it refills the slot it just freed with slice it + PF, multiplies
+  // slice it, then commits slice it + 1 (loaded PF - 1 iterations earlier) to the other LDS stage. The loop is
+  // unrolled by PF so every slot index is a compile-time constant (registers, never scratch).
+#pragma unroll
+  for (int s = 0; s < PF; ++s)
+    if (s < nk) gload(ra[s], rb[s]);
+  if (nk > 0) sstore(0, ra[0], rb[0]);
+  __syncthreads();
+
+  for (int base = 0; base < nk; base += PF) {
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+      const int it = base + s;
+      if (it < nk) {
+        if (it + PF < nk) gload(ra[s], rb[s]);
+        compute(it & 1);
+        if (it + 1 < nk) sstore((it + 1) & 1, ra[(s + 1) % PF], rb[(s + 1) % PF]);
+        __syncthreads();
+      }
+    }
   }
 
   // Epilogue. Lane holds, for MFMA block (i, j), pixels nb..nb+3 of output channel o.
@@ -242,7 +249,7 @@ struct Config {
   KernelFn fp16, bf16;
 };
 
-template <int TP, int TC, int BK, int WP, int WC>
+template <int TP, int TC, int BK, int WP, int WC, int PF>
 Config make_config(int version) {
   using S = Shape<TP, TC, BK, WP, WC>;
   Config c;
@@ -254,27 +261,28 @@ Config make_config(int version) {
   c.info.waves_n = WP;
   c.info.threads = S::NT;
   c.info.lds_bytes = S::kLds;
+  c.info.stages = PF;
   c.info.version = version;
-  c.fp16 = &igemm_kernel<Fp16, TP, TC, BK, WP, WC>;
-  c.bf16 = &igemm_kernel<Bf16, TP, TC, BK, WP, WC>;
+  c.fp16 = &igemm_kernel<Fp16, TP, TC, BK, WP, WC, PF>;
+  c.bf16 = &igemm_kernel<Bf16, TP, TC, BK, WP, WC, PF>;
   return c;
 }
 
 const std::vector<Config>& configs() {
   static const std::vector<Config> table = [] {
     std::vector<Config> t;
-    //            pixels x channels x k, waves (pixels x channels)
-    t.push_back(make_config<128, 128, 32, 2, 2>(1));
-    t.push_back(make_config<128, 128, 64, 2, 2>(1));
-    t.push_back(make_config<128, 64, 32, 2, 2>(1));
-    t.push_back(make_config<128, 64, 64, 2, 2>(1));
-    t.push_back(make_config<64, 128, 32, 2, 2>(1));
-    t.push_back(make_config<64, 128, 64, 2, 2>(1));
-    t.push_back(make_config<64, 64, 32, 2, 2>(1));
-    t.push_back(make_config<64, 64, 64, 2, 2>(1));
-    t.push_back(make_config<256, 128, 32, 4, 2>(1));
-    t.push_back(make_config<128, 256, 32, 2, 4>(1));
-    t.push_back(make_config<32, 64, 64, 1, 2>(1));
+    //            pixels x channels x k, waves (pixels x channels), register pipeline depth
+    t.push_back(make_config<128, 128, 32, 2, 2, 4>(2));
+    t.push_back(make_config<128, 128, 64, 2, 2, 3>(2));
+    t.push_back(make_config<128, 64, 32, 2, 2, 4>(2));
+    t.push_back(make_config<128, 64, 64, 2, 2, 3>(2));
+    t.push_back(make_config<64, 128, 32, 2, 2, 4>(2));
+    t.push_back(make_config<64, 128, 64, 2, 2, 3>(2));
+    t.push_back(make_config<64, 64, 32, 2, 2, 4>(2));
+    t.push_back(make_config<64, 64, 64, 2, 2, 4>(2));
+    t.push_back(make_config<256, 128, 32, 4, 2, 3>(2));
+    t.push_back(make_config<128, 256, 32, 2, 4, 3>(2));
+    t.push_back(make_config<32, 64, 64, 1, 2, 4>(2));
     return t;
   }();
   return table;

@@ -112,23 +112,60 @@ __device__ __forceinline__ void weight_chunk(const WJob& j, long long blk) {
   *reinterpret_cast<u32x4*>(j.wk + orow * j.Cp + c8) = v;
 }
 
+// One output channel per workgroup: its C*RS filter taps are contiguous in OIHW, so they are read with
+// coalesced loads into LDS and leave as 16-byte [rs][8 channels] vectors (used when C*RS fits kWElems).
+constexpr int kWElems = 8192;
+
+__device__ __forceinline__ void weight_filter(const WJob& j, long long o, uint16_t* buf) {
+  const int n = j.C * j.RS;
+  const uint16_t* src = j.w + o * n;
+  for (int i = threadIdx.x; i < n; i += kThreads) buf[i] = src[i];
+  __syncthreads();
+  const int cv = j.Cp / 8;
+  uint16_t* dst = j.wk + o * static_cast<long long>(j.RS) * j.Cp;
+  for (int t = threadIdx.x; t < j.RS * cv; t += kThreads) {
+    const int rs = t / cv, c8 = (t - rs * cv) * 8;
+    u32x4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = c8 + 2 * q;
+      const uint32_t lo = c < j.C ? buf[c * j.RS + rs] : 0u;
+      const uint32_t hi = c + 1 < j.C ? buf[(c + 1) * j.RS + rs] : 0u;
+      v[q] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(dst + rs * j.Cp + c8) = v;
+  }
+}
+
+inline bool w_per_filter(const WJob& j) { return j.C * j.RS <= kWElems; }
+
+inline long long w_launch_blocks(const WJob& j) { return w_per_filter(j) ? j.O : w_blocks(j); }
+
+__device__ __forceinline__ void weight_any(const WJob& j, long long blk, uint16_t* buf) {
+  if (j.C * j.RS <= kWElems) weight_filter(j, blk, buf);
+  else weight_chunk(j, blk);
+}
+
 __global__ __launch_bounds__(kThreads) void repack_act_kernel(ActJob j) {
   __shared__ uint16_t tile[kTile][kTile + 2];
   if (j.small) act_small(j, blockIdx.x);
   else act_tiled(j, blockIdx.x, tile);
 }
 
-__global__ __launch_bounds__(kThreads) void repack_w_kernel(WJob j) { weight_chunk(j, blockIdx.x); }
+__global__ __launch_bounds__(kThreads) void repack_w_kernel(WJob j) {
+  __shared__ uint16_t buf[kWElems];
+  weight_any(j, blockIdx.x, buf);
+}
 
-// Both repacks in one dispatch: blocks [0, act_blocks) repack activations, the rest repack weights.
+// Both repacks in one dispatch: blocks [0, n_act) repack activations, the rest repack weights.
 __global__ __launch_bounds__(kThreads) void repack_both_kernel(ActJob a, WJob w, long long n_act) {
-  __shared__ uint16_t tile[kTile][kTile + 2];
+  __shared__ uint16_t buf[kWElems > kTile * (kTile + 2) ? kWElems : kTile * (kTile + 2)];
   const long long blk = blockIdx.x;
   if (blk < n_act) {
     if (a.small) act_small(a, blk);
-    else act_tiled(a, blk, tile);
+    else act_tiled(a, blk, reinterpret_cast<uint16_t(*)[kTile + 2]>(buf));
   } else {
-    weight_chunk(w, blk - n_act);
+    weight_any(w, blk - n_act, buf);
   }
 }
 
@@ -183,7 +220,7 @@ extern "C" int gie_hip_repack_w_oihw_to_orsc(const void* w, void* wk, int out_ch
                                              void* stream) {
   WJob j;
   if (int rc = make_w(w, wk, out_channels, channels, rs, c_pad, &j)) return rc;
-  const long long blocks = w_blocks(j);
+  const long long blocks = w_launch_blocks(j);
   if (blocks > 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
   hipLaunchKernelGGL(repack_w_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, static_cast<hipStream_t>(stream), j);
   return launched();
@@ -196,7 +233,7 @@ extern "C" int gie_hip_repack_act_and_w(const void* x, void* xn, const void* w, 
   WJob wj;
   if (int rc = make_act(x, xn, g->batch, g->in_channels, g->in_h * g->in_w, g->c_pad, &a)) return rc;
   if (int rc = make_w(w, wk, g->out_channels, g->in_channels, g->kernel_h * g->kernel_w, g->c_pad, &wj)) return rc;
-  const long long na = act_blocks(a), nw = w_blocks(wj);
+  const long long na = act_blocks(a), nw = w_launch_blocks(wj);
   if (na + nw > 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
   hipLaunchKernelGGL(repack_both_kernel, dim3(unsigned(na + nw)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                      a, wj, na);

@@ -206,11 +206,13 @@ void register_mfma_family(std::vector<KernelDesc>& out) {
     KernelDesc k;
     k.name = std::string("mfma_") + to_string(en.precision) + "_" + std::to_string(en.info.tile_m) + "x" +
              std::to_string(en.info.tile_n) + "x" + std::to_string(en.info.tile_k) + "_w" +
-             std::to_string(en.info.waves_m) + "x" + std::to_string(en.info.waves_n) + "_sk" + std::to_string(en.split);
+             std::to_string(en.info.waves_m) + "x" + std::to_string(en.info.waves_n) + "_s" +
+             std::to_string(en.info.stages) + "_sk" + std::to_string(en.split);
     k.backend = Backend::kTensorCore;
     k.version = en.info.version;
     k.params = {{"block_m", en.info.tile_m}, {"block_n", en.info.tile_n}, {"block_k", en.info.tile_k},
-                {"waves_m", en.info.waves_m}, {"waves_n", en.info.waves_n}, {"split_k", en.split}};
+                {"waves_m", en.info.waves_m}, {"waves_n", en.info.waves_n}, {"stages", en.info.stages},
+                {"split_k", en.split}};
     k.threads_per_block = en.info.threads;
     k.tile_m = en.info.tile_m;
     k.tile_n = en.info.tile_n;

@@ -65,7 +65,7 @@ class GieConvGeom(ctypes.Structure):
 
 class GieIgemmConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
-        "tile_m", "tile_n", "tile_k", "waves_m", "waves_n", "threads", "lds_bytes", "version")]
+        "tile_m", "tile_n", "tile_k", "waves_m", "waves_n", "threads", "lds_bytes", "stages", "version")]
 
 
 _vp = ctypes.c_void_p
@@ -115,6 +115,7 @@ _CAPI = {
     "gie_device_arch": ([_i, _cp, _sz], _i),
     "gie_device_cu_count": ([_i, _ip], _i),
     "gie_build_fingerprint": ([_cp, _sz], _i),
+    "gie_testing_add_faulty_kernels": ([_i], _i),
     "gie_graph_create": ([ctypes.POINTER(_vp)], _i),
     "gie_graph_destroy": ([_vp], _i),
     "gie_graph_capture_chain": ([_vp, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
@@ -159,6 +160,7 @@ _HIP = {
     "gie_hip_ceiling_mfma": ([_i, _i, _vp, _vp], _i),
     "gie_hip_ceiling_copy": ([_vp, _vp, _sz, _vp], _i),
     "gie_hip_ceiling_empty": ([_vp], _i),
+    "gie_hip_fill_u16": ([_vp, ctypes.c_int64, ctypes.c_uint16, _vp], _i),
 }
 
 _libs = None
@@ -435,7 +437,8 @@ class ConvTensors:
     def tensors(self):
         p = self.p
         return (tensor(self.dx.addr, p, "x"), tensor(self.dw.addr, p, "w"),
-                tensor(self.db.addr, p, "b") if self.db is not None else None, tensor(self.dy.addr, p, "y"))
+                tensor(self.db.addr, p, "b") if (self.db is not None and p.has_bias) else None,
+                tensor(self.dy.addr, p, "y"))
 
     def bias_addr(self):
         return self.db.addr if (self.db is not None and self.p.has_bias) else None
@@ -527,10 +530,11 @@ class Plan:
 
     def execute(self, t: ConvTensors, ws: DeviceBuffer | None, stream: Stream | None = None, **override):
         x, w, b, y = t.tensors()
-        for k, v in override.items():
-            {"x": x, "w": w, "b": b, "y": y}[k[0]].__setattr__(k[2:], v)  # e.g. x_data=..., y_c=...
+        pass_bias = override.pop("bias", True)
+        for k, v in override.items():  # e.g. x_data=..., y_c=... patch one field of one tensor descriptor
+            setattr({"x": x, "w": w, "b": b, "y": y}[k[0]], k[2:], v)
         check(capi().gie_plan_execute(self.h, ctypes.byref(x), ctypes.byref(w),
-                                      ctypes.byref(b) if (b is not None and override.get("bias", True)) else None,
+                                      ctypes.byref(b) if (b is not None and pass_bias) else None,
                                       ctypes.byref(y), ws.addr if ws else None, ws.nbytes if ws else 0,
                                       stream.h if stream else None), "ExecutionPlan::execute")
 

@@ -128,6 +128,11 @@ int gie_device_arch(int device, char* buf, size_t n);
 int gie_device_cu_count(int device, int* cus);
 int gie_build_fingerprint(char* buf, size_t n);
 
+/* TESTING ONLY (kernel_registry_for_testing, kernel_registry.h:78-80): appends a deliberately faulty tensor_core
+   kernel to the registry so tests can prove the autotuner never selects it. kind 0: fast but wrong (fills y with
+   a constant), kind 1: its launch throws. Names: "test_garbage_<p>" / "test_throwing_<p>" per precision. */
+int gie_testing_add_faulty_kernels(int kind);
+
 /* ---- HipGraphExecutor (cuda_graph.h:14-46) over a chain of plan executions ---- */
 int gie_graph_create(void** graph);
 int gie_graph_destroy(void* graph);

@@ -53,6 +53,7 @@ typedef struct gie_igemm_config {
   int waves_m, waves_n; /* wave64 grid inside a workgroup */
   int threads;          /* waves_m * waves_n * 64 */
   int lds_bytes;        /* LDS per workgroup (two stages of the A and B tiles) */
+  int stages;           /* K slices in flight in registers ahead of the LDS stage being multiplied */
   int version;          /* bumps when the kernel's code changes behaviour or speed */
 } gie_igemm_config;
 
@@ -100,6 +101,9 @@ int gie_hip_reference_conv(int dtype, const gie_conv_geom* g, const void* x, con
 int gie_hip_ceiling_mfma(int blocks, int iters, float* sink, void* stream);
 int gie_hip_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream);
 int gie_hip_ceiling_empty(void* stream);
+
+/* dst[i] = value for i < n (16-bit elements, any 2-byte alignment). A graph-safe fill (no memset node). */
+int gie_hip_fill_u16(void* dst, int64_t n, uint16_t value, void* stream);
 
 #ifdef __cplusplus
 }
