@@ -247,25 +247,28 @@ int gie_plan_time_stages(void* plan, const void* x, const void* w, const void* b
     ExecutionPlan& pl = plan_of(plan);
     GIE_REQUIRE(iters > 0 && us3, StatusCode::kInvalidArgument, "bad iteration count");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipEvent_t ev[4];
-    for (auto& e : ev) GIE_HIP_CHECK(hipEventCreate(&e));
+    // Every call gets its own four events and all calls are queued back to back (no host sync in between),
+    // so each stage interval is that kernel's time on the stream as it runs inside a steady stream of calls.
+    std::vector<hipEvent_t> ev(size_t(iters) * 4, nullptr);
     struct G {
-      hipEvent_t* e;
+      std::vector<hipEvent_t>& e;
       ~G() {
-        for (int i = 0; i < 4; ++i) (void)hipEventDestroy(e[i]);
+        for (hipEvent_t x : e)
+          if (x) (void)hipEventDestroy(x);
       }
     } guard{ev};
+    for (auto& e : ev) GIE_HIP_CHECK(hipEventCreate(&e));
+    pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s);  // warm
+    for (int it = 0; it < iters; ++it) pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, &ev[size_t(it) * 4]);
+    GIE_HIP_CHECK(hipEventSynchronize(ev.back()));
     double acc[3] = {0, 0, 0};
     for (int it = 0; it < iters; ++it) {
-      pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, ev);
-      GIE_HIP_CHECK(hipEventSynchronize(ev[3]));
-      float a = 0, b = 0, c = 0;
-      GIE_HIP_CHECK(hipEventElapsedTime(&a, ev[0], ev[1]));
-      GIE_HIP_CHECK(hipEventElapsedTime(&b, ev[1], ev[2]));
-      GIE_HIP_CHECK(hipEventElapsedTime(&c, ev[2], ev[3]));
-      acc[0] += a * 1e3;
-      acc[1] += b * 1e3;
-      acc[2] += c * 1e3;
+      hipEvent_t* e = &ev[size_t(it) * 4];
+      for (int k = 0; k < 3; ++k) {
+        float ms = 0;
+        GIE_HIP_CHECK(hipEventElapsedTime(&ms, e[k], e[k + 1]));
+        acc[k] += ms * 1e3;
+      }
     }
     for (int i = 0; i < 3; ++i) us3[i] = acc[i] / iters;
   });

@@ -7,13 +7,14 @@
 // pixels of one output channel, which are contiguous in NCHW and leave as one 8-byte store.
 //
 // Workgroup: WP x WC wave64s own a TP(pixels) x TC(channels) output tile and walk K in BK slices.
-//   * global -> registers: each thread owns fixed tile rows and one 16-byte K chunk column; activation rows
-//     gather from the NHWC buffer at the (r, s) tap of that chunk (zero outside the image / past K), weight
-//     rows are contiguous along K. The tap cursor advances incrementally (no per-slice division or LUT).
-//   * registers -> LDS: two stages, rows padded by 16 bytes so the 16-lane ds_read_b128 fragment reads of an
-//     MFMA operand hit distinct banks.
-//   * the next slice's global loads are issued before the current slice's MFMAs, so HBM/L2 latency hides
-//     behind matrix work; one barrier per slice.
+//   * global -> registers with buffer loads: a lane whose row is outside the image / past the slice range /
+//     past M gets an out-of-range offset and the hardware returns zeros, so the loads carry no branches and
+//     the compiler's wait counting stays exact. Each thread owns fixed tile rows and one 16-byte K-chunk
+//     column; the chunk's tap offset (r, s, c0) is the same for all of the thread's rows and advances without
+//     division (branch-free when c_pad is a multiple of BK).
+//   * PF register slots hold the next K slices in flight while LDS holds the slice being multiplied (two LDS
+//     stages, rows padded by 16 bytes so the 16-lane ds_read_b128 fragment reads hit distinct banks); one
+//     barrier per slice.
 //   * epilogue: bias + ReLU on the FP32 accumulators, one RNE rounding, NCHW store (split == 1); or FP32
 //     partials for split-K, summed by splitk_reduce.hip.
 // Split-K slices follow the reference's partition rule [floor(kt*z/S), floor(kt*(z+1)/S))
@@ -30,11 +31,21 @@ namespace {
 
 struct Geom {
   int B, C, H, W, O, KH, KW, SH, SW, PH, PW, OH, OW, Cp, relu;
-  int HWo;      // OH * OW
-  int N;        // B * HWo output pixels
-  int Kp;       // KH * KW * Cp
-  int img;      // H * W * Cp elements per repacked image
+  int HWo;       // OH * OW
+  int N;         // B * HWo output pixels
+  int Kp;        // KH * KW * Cp
+  int img;       // H * W * Cp elements per repacked image
+  int xn_bytes;  // size of the repacked activations (buffer range)
+  int wk_bytes;  // size of the repacked weights
 };
+
+// gfx9-family buffer descriptor word 3 (raw buffer, 32-bit data format): reads past num_records return 0.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kOutOfRange = 0x80000000;
+
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
 
 template <int TP, int TC, int BK, int WP, int WC>
 struct Shape {
@@ -50,7 +61,7 @@ struct Shape {
   static_assert((TP * CPR) % NT == 0 && (TC * CPR) % NT == 0 && NT % CPR == 0, "chunks must divide over threads");
 };
 
-template <typename E, int TP, int TC, int BK, int WP, int WC, int PF>
+template <typename E, int TP, int TC, int BK, int WP, int WC, int PF, bool EXACT>
 __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __restrict__ xn,
                                                              const uint16_t* __restrict__ wk,
                                                              const uint16_t* __restrict__ bias,
@@ -69,35 +80,37 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
   const int kt_begin = int((static_cast<long long>(ktiles) * blockIdx.z) / split);
   const int kt_end = int((static_cast<long long>(ktiles) * (blockIdx.z + 1)) / split);
   const int nk = kt_end - kt_begin;
-  const int kchunks = g.Kp >> 3;
   const int kc = tid % S::CPR;
+  // chunk range of this slice set (chunks past the padded K or the slice end read as zeros)
+  const int q_end = min(kt_end * S::CPR, g.Kp >> 3);
 
-  // Fixed rows of this thread: pixel origin of each activation row, base of each weight row.
-  const uint16_t* a_img[S::LA];
-  int a_hb[S::LA], a_wb[S::LA];
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xn), 0, g.xn_bytes,
+                                                                      kBufferWord3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(wk), 0, g.wk_bytes,
+                                                                      kBufferWord3);
+
+  // Fixed rows of this thread: element offset of tap (0,0) channel 0 for each activation row, and the input
+  // origin (hb, wb) for the bounds test; element offset of each weight row (or -1 past M).
+  int a_off[S::LA], a_hb[S::LA], a_wb[S::LA];
 #pragma unroll
   for (int i = 0; i < S::LA; ++i) {
-    const int n = n0 + (tid + i * S::NT) / S::CPR;
-    if (n < g.N) {
-      const int b = n / g.HWo;
-      const int p = n - b * g.HWo;
-      const int oh = p / g.OW, ow = p - (p / g.OW) * g.OW;
-      a_img[i] = xn + static_cast<long long>(b) * g.img;
-      a_hb[i] = oh * g.SH - g.PH;
-      a_wb[i] = ow * g.SW - g.PW;
-    } else {
-      a_img[i] = xn;
-      a_hb[i] = -0x40000000;  // every tap lands outside the image -> zero row
-      a_wb[i] = 0;
-    }
+    // selects, not branches: a divergent branch here makes the compiler clone the load paths below
+    const int n_raw = n0 + (tid + i * S::NT) / S::CPR;
+    const bool nv = n_raw < g.N;
+    const int n = nv ? n_raw : 0;
+    const int b = n / g.HWo;
+    const int p = n - b * g.HWo;
+    const int oh = p / g.OW, ow = p - (p / g.OW) * g.OW;
+    const int hb = oh * g.SH - g.PH, wb = ow * g.SW - g.PW;
+    a_hb[i] = nv ? hb : -0x40000000;  // an invalid row: every tap lands outside the image -> zeros
+    a_wb[i] = wb;
+    a_off[i] = b * g.img + (hb * g.W + wb) * g.Cp;
   }
-  const uint16_t* b_row[S::LB];
-  bool b_ok[S::LB];
+  int b_off[S::LB];
 #pragma unroll
   for (int i = 0; i < S::LB; ++i) {
     const int o = m0 + (tid + i * S::NT) / S::CPR;
-    b_ok[i] = o < g.O;
-    b_row[i] = wk + static_cast<long long>(b_ok[i] ? o : 0) * g.Kp;
+    b_off[i] = o < g.O ? o * g.Kp : -1;
   }
 
   // K cursor of this thread's chunk column: chunk q -> tap (r, s), channel offset c0.
@@ -111,25 +124,36 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
   u32x4 ra[PF][S::LA], rb[PF][S::LB];
   // Loads the slice at the cursor into one register slot, then advances the cursor by one slice.
   auto gload = [&](u32x4(&A)[S::LA], u32x4(&B)[S::LB]) {
-    const bool kok = q < kchunks;
+    // bitwise &, not &&: short-circuit evaluation would become divergent control flow around the loads
+    const bool kok = q < q_end;
+    const int tap = (r * g.W + s) * g.Cp + c0;
 #pragma unroll
     for (int i = 0; i < S::LA; ++i) {
-      const int ih = a_hb[i] + r, iw = a_wb[i] + s;
-      const bool ok = kok && ih >= 0 && ih < g.H && iw >= 0 && iw < g.W;
-      A[i] = ok ? *reinterpret_cast<const u32x4*>(a_img[i] + (ih * g.W + iw) * g.Cp + c0) : u32x4{0, 0, 0, 0};
+      const bool ok = kok & (static_cast<unsigned>(a_hb[i] + r) < static_cast<unsigned>(g.H)) &
+                      (static_cast<unsigned>(a_wb[i] + s) < static_cast<unsigned>(g.W));
+      A[i] = load16(xr, ok ? (a_off[i] + tap) * 2 : kOutOfRange);
     }
 #pragma unroll
     for (int i = 0; i < S::LB; ++i) {
-      const bool ok = kok && b_ok[i];
-      B[i] = ok ? *reinterpret_cast<const u32x4*>(b_row[i] + q * 8) : u32x4{0, 0, 0, 0};
+      const bool ok = kok & (b_off[i] >= 0);
+      B[i] = load16(wr, ok ? (b_off[i] + q * 8) * 2 : kOutOfRange);
     }
     q += S::CPR;
     c0 += BK;
-    while (c0 >= g.Cp) {
-      c0 -= g.Cp;
-      if (++s == g.KW) {
-        s = 0;
-        ++r;
+    if (EXACT) {  // c_pad % BK == 0: a slice never straddles two taps
+      const bool wrap = c0 >= g.Cp;
+      c0 = wrap ? c0 - g.Cp : c0;  // back to this thread's chunk column kc*8 of the next tap
+      s += wrap ? 1 : 0;
+      const bool wrap2 = s == g.KW;
+      s = wrap2 ? 0 : s;
+      r += wrap2 ? 1 : 0;
+    } else {
+      while (c0 >= g.Cp) {
+        c0 -= g.Cp;
+        if (++s == g.KW) {
+          s = 0;
+          ++r;
+        }
       }
     }
   };
@@ -170,30 +194,33 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
     }
   };
 
-  // Software pipeline: PF register slots hold the next K slices in flight (slot it % PF holds slice it), LDS
-  // holds the slice being multiplied. Iteration it refills the slot it just freed with slice it + PF, multiplies
-  // slice it, then commits slice it + 1 (loaded PF - 1 iterations earlier) to the other LDS stage. The loop is
-  // unrolled by PF so every slot index is a compile-time constant (registers, never scratch).
+  // Software pipeline: register slot it % PF holds slice it. Iteration it refills the slot it just freed with
+  // slice it + PF, multiplies slice it from LDS, commits slice it + 1 to the other LDS stage, and meets the
+  // others at one barrier. Loads and stores past the last slice read zeros and are never multiplied; only the
+  // multiply is guarded (a uniform branch). The loop is unrolled by PF so every slot index is a constant.
 #pragma unroll
-  for (int s = 0; s < PF; ++s)
-    if (s < nk) gload(ra[s], rb[s]);
-  if (nk > 0) sstore(0, ra[0], rb[0]);
+  for (int st = 0; st < PF; ++st) gload(ra[st], rb[st]);
+  sstore(0, ra[0], rb[0]);
   __syncthreads();
 
   for (int base = 0; base < nk; base += PF) {
 #pragma unroll
-    for (int s = 0; s < PF; ++s) {
-      const int it = base + s;
-      if (it < nk) {
-        if (it + PF < nk) gload(ra[s], rb[s]);
-        compute(it & 1);
-        if (it + 1 < nk) sstore((it + 1) & 1, ra[(s + 1) % PF], rb[(s + 1) % PF]);
-        __syncthreads();
-      }
+    for (int st = 0; st < PF; ++st) {
+      const int it = base + st;
+      gload(ra[st], rb[st]);
+      if (it < nk) compute(it & 1);
+      sstore((it + 1) & 1, ra[(st + 1) % PF], rb[(st + 1) % PF]);
+      __syncthreads();
     }
   }
 
   // Epilogue. Lane holds, for MFMA block (i, j), pixels nb..nb+3 of output channel o.
+  float bv[S::FC];
+#pragma unroll
+  for (int j = 0; j < S::FC; ++j) {
+    const int o = m0 + wc * S::WTC + j * 16 + (lane & 15);
+    bv[j] = (split == 1 && bias != nullptr && o < g.O) ? E::to_f32(bias[o]) : 0.0f;
+  }
   const long long total = static_cast<long long>(g.N) * g.O;
 #pragma unroll
   for (int i = 0; i < S::FP; ++i) {
@@ -223,7 +250,11 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
       } else {
         uint16_t h[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = epilogue<E>(v[e], bias, o, g.relu);
+        for (int e = 0; e < 4; ++e) {
+          float a = v[e] + bv[j];  // bias added to the FP32 accumulator, then ReLU, then one rounding
+          if (g.relu) a = fmaxf(a, 0.0f);
+          h[e] = E::from_f32(a);
+        }
         uint16_t* dst = y + idx;
         if (whole && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
           *reinterpret_cast<u32x2*>(dst) = u32x2{uint32_t(h[0]) | (uint32_t(h[1]) << 16),
@@ -246,7 +277,7 @@ typedef void (*KernelFn)(const uint16_t*, const uint16_t*, const uint16_t*, uint
 
 struct Config {
   gie_igemm_config info;
-  KernelFn fp16, bf16;
+  KernelFn fp16[2], bf16[2];  // [EXACT]: c_pad % tile_k == 0 takes the branch-free cursor
 };
 
 template <int TP, int TC, int BK, int WP, int WC, int PF>
@@ -263,8 +294,10 @@ Config make_config(int version) {
   c.info.lds_bytes = S::kLds;
   c.info.stages = PF;
   c.info.version = version;
-  c.fp16 = &igemm_kernel<Fp16, TP, TC, BK, WP, WC, PF>;
-  c.bf16 = &igemm_kernel<Bf16, TP, TC, BK, WP, WC, PF>;
+  c.fp16[0] = &igemm_kernel<Fp16, TP, TC, BK, WP, WC, PF, false>;
+  c.fp16[1] = &igemm_kernel<Fp16, TP, TC, BK, WP, WC, PF, true>;
+  c.bf16[0] = &igemm_kernel<Bf16, TP, TC, BK, WP, WC, PF, false>;
+  c.bf16[1] = &igemm_kernel<Bf16, TP, TC, BK, WP, WC, PF, true>;
   return c;
 }
 
@@ -272,17 +305,17 @@ const std::vector<Config>& configs() {
   static const std::vector<Config> table = [] {
     std::vector<Config> t;
     //            pixels x channels x k, waves (pixels x channels), register pipeline depth
-    t.push_back(make_config<128, 128, 32, 2, 2, 4>(2));
-    t.push_back(make_config<128, 128, 64, 2, 2, 3>(2));
-    t.push_back(make_config<128, 64, 32, 2, 2, 4>(2));
-    t.push_back(make_config<128, 64, 64, 2, 2, 3>(2));
-    t.push_back(make_config<64, 128, 32, 2, 2, 4>(2));
-    t.push_back(make_config<64, 128, 64, 2, 2, 3>(2));
-    t.push_back(make_config<64, 64, 32, 2, 2, 4>(2));
-    t.push_back(make_config<64, 64, 64, 2, 2, 4>(2));
-    t.push_back(make_config<256, 128, 32, 4, 2, 3>(2));
-    t.push_back(make_config<128, 256, 32, 2, 4, 3>(2));
-    t.push_back(make_config<32, 64, 64, 1, 2, 4>(2));
+    t.push_back(make_config<128, 128, 32, 2, 2, 4>(3));
+    t.push_back(make_config<128, 128, 64, 2, 2, 3>(3));
+    t.push_back(make_config<128, 64, 32, 2, 2, 4>(3));
+    t.push_back(make_config<128, 64, 64, 2, 2, 3>(3));
+    t.push_back(make_config<64, 128, 32, 2, 2, 4>(3));
+    t.push_back(make_config<64, 128, 64, 2, 2, 3>(3));
+    t.push_back(make_config<64, 64, 32, 2, 2, 4>(3));
+    t.push_back(make_config<64, 64, 64, 2, 2, 4>(3));
+    t.push_back(make_config<256, 128, 32, 4, 2, 3>(3));
+    t.push_back(make_config<128, 256, 32, 2, 4, 3>(3));
+    t.push_back(make_config<32, 64, 64, 1, 2, 4>(3));
     return t;
   }();
   return table;
@@ -320,7 +353,7 @@ extern "C" int gie_hip_igemm_occupancy(int index, int dtype, int* blocks_per_cu)
   if (index < 0 || index >= int(configs().size()) || !blocks_per_cu) return GIE_HIP_EINVAL;
   if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
   const Config& c = configs()[size_t(index)];
-  KernelFn fn = dtype == GIE_HIP_FP16 ? c.fp16 : c.bf16;
+  KernelFn fn = dtype == GIE_HIP_FP16 ? c.fp16[1] : c.bf16[1];
   if (int rc = set_lds_limit(fn, c.info.lds_bytes)) return rc;
   int n = 0;
   const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn),
@@ -359,20 +392,25 @@ extern "C" int gie_hip_conv_igemm(int config, int dtype, const gie_conv_geom* gg
   if (g.B <= 0 || g.C <= 0 || g.H <= 0 || g.W <= 0 || g.O <= 0 || g.KH <= 0 || g.KW <= 0 || g.SH <= 0 || g.SW <= 0 ||
       g.PH < 0 || g.PW < 0 || g.OH <= 0 || g.OW <= 0 || g.Cp < g.C || (g.Cp & 7) != 0)
     return GIE_HIP_EINVAL;
-  // every index the kernel forms in 32 bits must fit
+  // every offset the kernel forms in 32 bits must fit, and the buffer ranges stay below the out-of-range marker
   const long long hwo = static_cast<long long>(g.OH) * g.OW;
   const long long n = hwo * g.B;
   const long long kp = static_cast<long long>(g.KH) * g.KW * g.Cp;
   const long long img = static_cast<long long>(g.H) * g.W * g.Cp;
-  if (n > 0x7fffffffLL || kp > 0x7fffffffLL || img > 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
+  const long long xbytes = img * g.B * 2, wbytes = kp * g.O * 2;
+  if (n > 0x7fffffffLL || kp > 0x7fffffffLL || xbytes >= 0x7fffffffLL || wbytes >= 0x7fffffffLL)
+    return GIE_HIP_EUNSUPPORTED;
   g.HWo = int(hwo);
   g.N = int(n);
   g.Kp = int(kp);
   g.img = int(img);
+  g.xn_bytes = int(xbytes);
+  g.wk_bytes = int(wbytes);
   const long long gx = (n + c.info.tile_n - 1) / c.info.tile_n;
   const long long gy = (g.O + c.info.tile_m - 1) / c.info.tile_m;
   if (gx > 0x7fffffffLL || gy > 65535) return GIE_HIP_EUNSUPPORTED;
-  KernelFn fn = dtype == GIE_HIP_FP16 ? c.fp16 : c.bf16;
+  const int exact = (g.Cp % c.info.tile_k) == 0 ? 1 : 0;
+  KernelFn fn = dtype == GIE_HIP_FP16 ? c.fp16[exact] : c.bf16[exact];
   if (int rc = set_lds_limit(fn, c.info.lds_bytes)) return rc;
   hipLaunchKernelGGL(fn, dim3(unsigned(gx), unsigned(gy), unsigned(split)), dim3(c.info.threads), c.info.lds_bytes,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(xn),

@@ -157,7 +157,7 @@ def test_forced_backend_without_kernels_gives_clear_error():
 
 
 def test_explicit_kernel_overrides_everything():
-    p = P(1, 8, 8, 8, 8, 3, 3, 1, 1, 1, 1)
+    p = P(1, 64, 8, 8, 8, 3, 3, 1, 1, 1, 1)
     k, src, _ = gie.select(p, kernel=K16_SK4)
     assert k == K16_SK4 and src == "forced_kernel"
     expect_error("InvalidArgument", gie.select, p, kernel="no_such_kernel")
@@ -383,7 +383,7 @@ def test_create_then_use_on_fresh_streams():
     cases = []
     for k in (K16, K16_SK4, "mfma_fp16_128x64x64_w2x2_s3_sk1"):
         for v in range(2):
-            p = P(2, 16 + 8 * v, 9 + v, 11, 24, 3, 3, 1, 1, 1, 1)
+            p = P(2, 32 + 8 * v, 9 + v, 11, 24, 3, 3, 1, 1, 1, 1)
             cases.append((k, p, Bundle(p, 1000 + v, O.NORMAL)))
     bad = 0
     for it in range(36):
