@@ -147,14 +147,11 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
       const bool wrap2 = s == g.KW;
       s = wrap2 ? 0 : s;
       r += wrap2 ? 1 : 0;
-    } else {
-      while (c0 >= g.Cp) {
-        c0 -= g.Cp;
-        if (++s == g.KW) {
-          s = 0;
-          ++r;
-        }
-      }
+    } else {  // a slice spans several taps: recompute the tap from the chunk index (division, no branches)
+      const int rs2 = q / cvec;
+      c0 = (q - rs2 * cvec) * 8;
+      r = rs2 / g.KW;
+      s = rs2 - r * g.KW;
     }
   };
   auto sstore = [&](int st, const u32x4(&A)[S::LA], const u32x4(&B)[S::LB]) {

@@ -80,6 +80,7 @@ _OP = ctypes.POINTER(GieOptions)
 
 _CAPI = {
     "gie_last_error": ([], ctypes.c_char_p),
+    "gie_status_string": ([_i], ctypes.c_char_p),
     "gie_validate_problem": ([_PP], _i),
     "gie_problem_key": ([_PP, _cp, _sz], _i),
     "gie_conv2d_forward": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP], _i),

@@ -1,0 +1,131 @@
+"""C-ABI checks that need no GPU: both libraries load, every function the public headers declare is exported
+and bound by the Python layer, and the host-side logic behind the boundary (problem validation, problem keys,
+the library's CPU reference, the seeded data generator, the tile table) agrees with the oracle.
+
+Reference behaviour followed: conv2d.cpp:77-109 (key and validation), cpu_reference.cpp:13-56,
+testing.cu:75-105 (data generator), tensor_core_mma.cu:370-388 (tile table)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import gie
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = {"gie_capi.h": gie.LIBGIE, "gie_hip.h": gie.LIBGIE_HIP}
+
+
+def declared(header: str) -> list[str]:
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(gie_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header", sorted(HEADERS))
+def test_every_declared_symbol_is_exported(header):
+    names = declared(header)
+    assert len(names) > 10
+    lib = ctypes.CDLL(HEADERS[header], mode=ctypes.RTLD_GLOBAL)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_the_headers():
+    bound = set(gie._CAPI) | set(gie._HIP)
+    for header in HEADERS:
+        missing = [n for n in declared(header) if n not in bound]
+        assert not missing, (header, missing)
+    gie.libs()  # argtypes/restype applied to every bound symbol
+
+
+def _problems(rng, n):
+    """Random problems around the validation boundaries (zero, negative, oversize padding, dilation, groups)."""
+    good = ((1, 4), (1, 9), (1, 12), (1, 12), (1, 9), (1, 6), (1, 6), (1, 4), (1, 4), (0, 5), (0, 5), (1, 2),
+            (1, 2), (1, 2))
+    bad = ((-1, 1), (-1, 1), (-1, 1), (-1, 1), (-1, 1), (-1, 1), (-1, 1), (-1, 1), (-1, 1), (-2, 0), (-2, 0),
+           (0, 4), (0, 4), (0, 4))
+    out = []
+    for _ in range(n):
+        v = [int(rng.integers(*g)) for g in good]
+        for f in rng.choice(len(v), size=int(rng.integers(0, 3)), replace=False):
+            v[f] = int(rng.integers(*bad[f]))
+        out.append(v)
+    return out
+
+
+def test_validation_matches_oracle():
+    rng = np.random.default_rng(7)
+    seen = {0: 0, 1: 0, 2: 0}
+    for v in _problems(rng, 3000):
+        c = O.Conv(*v)
+        expect = O.validate(c)
+        p = gie.Problem(*v)
+        pc = p.c()
+        got = gie.capi().gie_validate_problem(ctypes.byref(pc))
+        assert got == expect, (v, got, expect)
+        seen[expect] += 1
+    assert min(seen.values()) > 20, seen  # every outcome exercised
+
+
+def test_problem_key_is_injective_on_geometry_and_flags():
+    base = dict(batch=2, in_channels=8, in_h=9, in_w=10, out_channels=4, kernel_h=3, kernel_w=3, stride_h=1,
+                stride_w=1, pad_h=1, pad_w=1)
+    keys = {gie.Problem(**base).key()}
+    for f in base:
+        d = dict(base)
+        d[f] += 1
+        keys.add(gie.Problem(**d).key())
+    keys.add(gie.Problem(**base, precision="bf16").key())
+    keys.add(gie.Problem(**base, has_bias=False).key())
+    keys.add(gie.Problem(**base, relu=False).key())
+    assert len(keys) == len(base) + 4
+
+
+@pytest.mark.parametrize("shape", [(1, 3, 8, 8, 4, 3, 3, 1, 1, 1, 1), (2, 7, 11, 13, 9, 3, 3, 2, 2, 0, 0),
+                                   (1, 4, 12, 12, 6, 1, 3, 1, 1, 0, 1), (2, 5, 9, 7, 3, 5, 5, 2, 1, 2, 2)])
+@pytest.mark.parametrize("bias,relu", [(True, True), (False, False)])
+def test_library_cpu_reference_matches_oracle(shape, bias, relu):
+    c = O.P(*shape, has_bias=bias, relu=relu, precision="fp32")
+    x, w, b = O.make_data(c, 11, O.NORMAL)
+    yo, so = O.conv2d(c, x, w, b if bias else None)
+    p = gie.Problem(*shape, precision="fp32", has_bias=bias, relu=relu)
+    yl, sl = gie.cpu_reference(p, x, w, b if bias else None)
+    np.testing.assert_allclose(yl, yo, rtol=0, atol=1e-5 * max(1.0, float(np.abs(so).max())))
+    np.testing.assert_allclose(sl, so, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("dist", [O.UNIFORM, O.NORMAL, O.SPARSE, O.POSITIVE])
+def test_host_data_generator_matches_oracle_bit_exact(precision, dist):
+    shape = (2, 5, 6, 7, 3, 3, 3, 1, 1, 1, 1)
+    c = O.P(*shape, precision=precision)
+    xo, wo, bo = O.make_data(c, 0xBEEF, dist, O.SCALING_BENCH)
+    p = gie.Problem(*shape, precision=precision)
+    xl, wl, bl = gie.make_host_data(p, 0xBEEF, dist=["uniform", "normal", "sparse_signed", "positive"][dist],
+                                    scaling="benchmark")
+    for a, b_ in ((xl, xo), (wl, wo), (bl.reshape(-1), bo)):
+        assert np.array_equal(a.reshape(-1).view(np.uint32), b_.reshape(-1).view(np.uint32))
+
+
+def test_tile_table_is_consistent():
+    cfgs = gie.igemm_configs()
+    assert len(cfgs) >= 8
+    for c in cfgs:
+        assert c["threads"] == 64 * c["waves_m"] * c["waves_n"]
+        assert c["tile_k"] % 32 == 0
+        assert c["tile_m"] % (16 * c["waves_m"]) == 0 and c["tile_n"] % (16 * c["waves_n"]) == 0
+        assert 0 < c["lds_bytes"] <= 160 * 1024
+
+
+def test_status_strings_and_fingerprint():
+    for rc in (0, -1, -2):
+        assert gie.hip().gie_hip_status_string(rc)
+    for rc in range(7):
+        assert gie.capi().gie_status_string(rc)
+    assert len(gie.build_fingerprint()) > 8
