@@ -51,12 +51,12 @@ def compulsory_bytes(p) -> float:
     return float((np.prod(p.x_shape()) + np.prod(p.w_shape()) + np.prod(p.y_shape()) + p.out_channels) * e)
 
 
-def run_config(gie, name, cfg, steps, warmup, stream, tune_cache):
+def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
     p = gie.Problem(**cfg, has_bias=True, relu=True)
     x, w, b = gie.make_host_data(p, SEED, "uniform", "benchmark")
     t = gie.ConvTensors(p, x, w, b)
-    # pick the kernel: autotuned (validated against the GPU double reference, cached), else the cost model
-    opts = dict(autotune=True, cache_path=tune_cache)
+    # pick the kernel: autotuned (validated against the GPU double reference, cached), or forced by name
+    opts = dict(kernel=kernel) if kernel else dict(autotune=True, cache_path=tune_cache)
     kernel, source, _ = gie.select(p, **opts)
     ws = gie.DeviceBuffer(gie.workspace_size(p, **opts))
     # correctness of the exact call being timed, against the library's GPU double reference
@@ -150,14 +150,27 @@ def _cpu_model() -> str:
 
 
 def load_traffic(kernel_name: str):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, if present."""
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, when that summary
+    was taken on the same registry kernel (else None: counters of another tiling say nothing about this one)."""
     path = os.path.join(ROOT, "profiles", "traffic_c2_fp16_3x3.json")
     try:
         with open(path) as f:
             d = json.load(f)
-        return d.get("bytes_per_launch")
     except (OSError, ValueError):
         return None
+    return d.get("bytes_per_launch") if d.get("kernel") == kernel_name else None
+
+
+def copy_probe(gie, mib: int, reps: int):
+    """A plain device copy of known size (`reps` launches of gie_hip_ceiling_copy over `mib` MiB): run under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE it gives the counters' scale factor on this machine."""
+    n = mib << 20
+    src, dst = gie.DeviceBuffer(n), gie.DeviceBuffer(n)
+    src.fill(0x3C)
+    for _ in range(reps):
+        gie.check_hip(gie.hip().gie_hip_ceiling_copy(src.addr, dst.addr, n, None), "ceiling_copy")
+    gie.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": reps}), flush=True)
 
 
 def main():
@@ -169,6 +182,10 @@ def main():
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--tune-cache", default=os.path.join(ROOT, "gpurun_out", "bench_tune_cache.json"))
+    ap.add_argument("--kernel", default=None,
+                    help="force this registry kernel (no autotune); only with a single --configs entry")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the Conv2D library is a "
@@ -178,8 +195,13 @@ def main():
     import gie
     gie.check(gie.capi().gie_set_device(0), "hipSetDevice")
     os.makedirs(os.path.dirname(args.tune_cache), exist_ok=True)
+    if args.copy_probe_mib > 0:
+        copy_probe(gie, args.copy_probe_mib, 5)
+        return
     stream = gie.Stream()
     names = list(CONFIGS) if args.configs == "all" else args.configs.split(",")
+    if args.kernel and names != [HEADLINE]:
+        ap.error(f"--kernel applies to --configs {HEADLINE} alone")
     if HEADLINE not in names:
         names.insert(0, HEADLINE)
     results = {}
@@ -188,7 +210,7 @@ def main():
         log(f"[bench] {name}: tuning + timing")
         steps = args.steps if name == HEADLINE else max(100, args.steps // 4)
         p, t, r = run_config(gie, name, CONFIGS[name], steps, args.warmup if name == HEADLINE else 50, stream,
-                             args.tune_cache)
+                             args.tune_cache, args.kernel)
         log(f"[bench] {name}: {r['kernel']} {r['us_per_call']:.2f} us/call {r['tflops']:.1f} TFLOP/s "
             f"(gemm {r['stage_us']['gemm_us']:.2f} us, repack {r['stage_us']['repack_us']:.2f} us) "
             f"rel_l2={r['rel_l2']:.2e}")
