@@ -13,8 +13,9 @@
 //     column; the chunk's tap offset (r, s, c0) is the same for all of the thread's rows and advances without
 //     division (branch-free when c_pad is a multiple of BK).
 //   * PF register slots hold the next K slices in flight while LDS holds the slice being multiplied (two LDS
-//     stages, rows padded by 16 bytes so the 16-lane ds_read_b128 fragment reads hit distinct banks); one
-//     barrier per slice.
+//     stages, unpadded rows with an xor swizzle of the 16-byte chunks so both the tile stores and the 16-row
+//     fragment reads are free of bank conflicts); fragments of the next 32-wide k step are read while the
+//     current one multiplies; one barrier per slice.
 //   * epilogue: bias + ReLU on the FP32 accumulators, one RNE rounding, NCHW store (split == 1); or FP32
 //     partials for split-K, summed by splitk_reduce.hip.
 // Split-K slices follow the reference's partition rule [floor(kt*z/S), floor(kt*(z+1)/S))
@@ -52,7 +53,7 @@ struct Shape {
   static constexpr int NT = WP * WC * 64;
   static constexpr int WTP = TP / WP, WTC = TC / WC;  // per-wave tile
   static constexpr int FP = WTP / 16, FC = WTC / 16;  // 16x16 MFMA blocks per wave
-  static constexpr int LDK = BK + 8;                  // LDS row pitch in 16-bit elements
+  static constexpr int LDK = BK;                      // LDS row pitch in 16-bit elements (swizzled)
   static constexpr int CPR = BK / 8;                  // 16-byte chunks per tile row
   static constexpr int LA = TP * CPR / NT, LB = TC * CPR / NT;
   static constexpr int kLds = 2 * (TP + TC) * LDK * 2;
@@ -154,16 +155,20 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
       s = rs2 - r * g.KW;
     }
   };
+  // LDS rows are BK elements, unpadded; 16-byte chunk c of row r sits at chunk c ^ swz(r). swz takes the row's
+  // position within a 256-byte bank period, so the row-major stores (CPR lanes per row) and the 16-row fragment
+  // reads (16 lanes, one chunk column) both spread over all 64 banks.
+  auto swz = [](int row) { return ((row * S::CPR) >> 4) % S::CPR; };
   auto sstore = [&](int st, const u32x4(&A)[S::LA], const u32x4(&B)[S::LB]) {
 #pragma unroll
     for (int i = 0; i < S::LA; ++i) {
       const int row = (tid + i * S::NT) / S::CPR;
-      *reinterpret_cast<u32x4*>(sA + (st * TP + row) * S::LDK + kc * 8) = A[i];
+      *reinterpret_cast<u32x4*>(sA + (st * TP + row) * S::LDK + ((kc ^ swz(row)) * 8)) = A[i];
     }
 #pragma unroll
     for (int i = 0; i < S::LB; ++i) {
       const int row = (tid + i * S::NT) / S::CPR;
-      *reinterpret_cast<u32x4*>(sB + (st * TC + row) * S::LDK + kc * 8) = B[i];
+      *reinterpret_cast<u32x4*>(sB + (st * TC + row) * S::LDK + ((kc ^ swz(row)) * 8)) = B[i];
     }
   };
 
@@ -173,42 +178,58 @@ __global__ __launch_bounds__(WP * WC * 64) void igemm_kernel(const uint16_t* __r
 #pragma unroll
     for (int j = 0; j < S::FC; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int frag_row = lane & 15, frag_k = (lane >> 4) * 8;
-  auto compute = [&](int st) {
-    const uint16_t* tA = sA + (st * TP + wp * S::WTP + frag_row) * S::LDK + frag_k;
-    const uint16_t* tB = sB + (st * TC + wc * S::WTC + frag_row) * S::LDK + frag_k;
+  // MFMA fragment of 16 rows: lane reads row (lane & 15), k-chunk kk*4 + (lane >> 4) of the 32-wide step kk.
+  // Fragment row bases are multiples of 16, so the swizzle depends on (lane & 15) only.
+  const int frag_row = lane & 15, frag_c = lane >> 4, frag_sw = swz(frag_row);
+  auto rdfrag = [&](int st, int kk, u32x4(&af)[S::FP], u32x4(&bf)[S::FC]) {
+    const int col = ((kk * 4 + frag_c) ^ frag_sw) * 8;
+    const uint16_t* tA = sA + (st * TP + wp * S::WTP + frag_row) * S::LDK + col;
+    const uint16_t* tB = sB + (st * TC + wc * S::WTC + frag_row) * S::LDK + col;
 #pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
-      u32x4 af[S::FP], bf[S::FC];
+    for (int i = 0; i < S::FP; ++i) af[i] = *reinterpret_cast<const u32x4*>(tA + i * 16 * S::LDK);
 #pragma unroll
-      for (int i = 0; i < S::FP; ++i) af[i] = *reinterpret_cast<const u32x4*>(tA + i * 16 * S::LDK + kk * 32);
+    for (int j = 0; j < S::FC; ++j) bf[j] = *reinterpret_cast<const u32x4*>(tB + j * 16 * S::LDK);
+  };
+  auto mma = [&](const u32x4(&af)[S::FP], const u32x4(&bf)[S::FC]) {
 #pragma unroll
-      for (int j = 0; j < S::FC; ++j) bf[j] = *reinterpret_cast<const u32x4*>(tB + j * 16 * S::LDK + kk * 32);
+    for (int i = 0; i < S::FP; ++i)
 #pragma unroll
-      for (int i = 0; i < S::FP; ++i)
+      for (int j = 0; j < S::FC; ++j) acc[i][j] = E::mfma(af[i], bf[j], acc[i][j]);
+  };
+  // One slice: refill register slot `st` with slice it + PF, multiply slice it from LDS stage it & 1 with the
+  // fragments of step kk + 1 read while step kk multiplies, commit slice it + 1 (slot (st + 1) % PF) to the
+  // other stage, meet at one barrier. No branch inside, so the compiler interleaves the LDS stores and the
+  // buffer loads with the MFMAs.
+  auto slice = [&](int it, u32x4(&rs_a)[S::LA], u32x4(&rs_b)[S::LB], const u32x4(&nx_a)[S::LA],
+                   const u32x4(&nx_b)[S::LB]) {
+    constexpr int KK = BK / 32;
+    u32x4 af[2][S::FP], bf[2][S::FC];
+    rdfrag(it & 1, 0, af[0], bf[0]);
+    gload(rs_a, rs_b);
 #pragma unroll
-        for (int j = 0; j < S::FC; ++j) acc[i][j] = E::mfma(af[i], bf[j], acc[i][j]);
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk + 1 < KK) rdfrag(it & 1, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+      mma(af[kk & 1], bf[kk & 1]);
     }
+    sstore((it + 1) & 1, nx_a, nx_b);
+    __syncthreads();
   };
 
-  // Software pipeline: register slot it % PF holds slice it. Iteration it refills the slot it just freed with
-  // slice it + PF, multiplies slice it from LDS, commits slice it + 1 to the other LDS stage, and meets the
-  // others at one barrier. Loads and stores past the last slice read zeros and are never multiplied; only the
-  // multiply is guarded (a uniform branch). The loop is unrolled by PF so every slot index is a constant.
+  // Register slot it % PF holds slice it (PF slices in flight). The loop runs whole groups of PF slices, then
+  // the remaining nk % PF slices one by one (uniform branches); loads past the last slice read zeros.
 #pragma unroll
   for (int st = 0; st < PF; ++st) gload(ra[st], rb[st]);
   sstore(0, ra[0], rb[0]);
   __syncthreads();
 
-  for (int base = 0; base < nk; base += PF) {
+  int base = 0;
+  for (; base + PF <= nk; base += PF) {
 #pragma unroll
-    for (int st = 0; st < PF; ++st) {
-      const int it = base + st;
-      gload(ra[st], rb[st]);
-      if (it < nk) compute(it & 1);
-      sstore((it + 1) & 1, ra[(st + 1) % PF], rb[(st + 1) % PF]);
-      __syncthreads();
-    }
+    for (int st = 0; st < PF; ++st) slice(base + st, ra[st], rb[st], ra[(st + 1) % PF], rb[(st + 1) % PF]);
+  }
+#pragma unroll
+  for (int st = 0; st + 1 < PF; ++st) {
+    if (base + st < nk) slice(base + st, ra[st], rb[st], ra[(st + 1) % PF], rb[(st + 1) % PF]);
   }
 
   // Epilogue. Lane holds, for MFMA block (i, j), pixels nb..nb+3 of output channel o.
@@ -302,17 +323,28 @@ const std::vector<Config>& configs() {
   static const std::vector<Config> table = [] {
     std::vector<Config> t;
     //            pixels x channels x k, waves (pixels x channels), register pipeline depth
-    t.push_back(make_config<128, 128, 32, 2, 2, 4>(3));
-    t.push_back(make_config<128, 128, 64, 2, 2, 3>(3));
-    t.push_back(make_config<128, 64, 32, 2, 2, 4>(3));
-    t.push_back(make_config<128, 64, 64, 2, 2, 3>(3));
-    t.push_back(make_config<64, 128, 32, 2, 2, 4>(3));
-    t.push_back(make_config<64, 128, 64, 2, 2, 3>(3));
-    t.push_back(make_config<64, 64, 32, 2, 2, 4>(3));
-    t.push_back(make_config<64, 64, 64, 2, 2, 4>(3));
-    t.push_back(make_config<256, 128, 32, 4, 2, 3>(3));
-    t.push_back(make_config<128, 256, 32, 2, 4, 3>(3));
-    t.push_back(make_config<32, 64, 64, 1, 2, 4>(3));
+    // four waves (one per SIMD)
+    t.push_back(make_config<128, 128, 32, 2, 2, 4>(4));
+    t.push_back(make_config<128, 128, 64, 2, 2, 3>(4));
+    t.push_back(make_config<128, 64, 32, 2, 2, 4>(4));
+    t.push_back(make_config<128, 64, 64, 2, 2, 3>(4));
+    t.push_back(make_config<64, 128, 32, 2, 2, 4>(4));
+    t.push_back(make_config<64, 128, 64, 2, 2, 3>(4));
+    t.push_back(make_config<64, 64, 32, 2, 2, 4>(4));
+    t.push_back(make_config<64, 64, 64, 2, 2, 4>(4));
+    t.push_back(make_config<32, 64, 64, 1, 2, 4>(4));
+    // eight waves (two per SIMD): twice the loads and LDS reads in flight per CU
+    t.push_back(make_config<256, 128, 32, 4, 2, 3>(4));
+    t.push_back(make_config<128, 256, 32, 2, 4, 3>(4));
+    t.push_back(make_config<128, 64, 64, 4, 2, 4>(4));
+    t.push_back(make_config<64, 128, 64, 2, 4, 3>(4));
+    t.push_back(make_config<128, 128, 64, 2, 4, 3>(4));
+    t.push_back(make_config<128, 128, 32, 4, 2, 4>(4));
+    t.push_back(make_config<64, 64, 64, 2, 4, 4>(4));
+    t.push_back(make_config<256, 64, 64, 4, 2, 2>(4));
+    t.push_back(make_config<64, 128, 128, 2, 4, 2>(4));
+    t.push_back(make_config<128, 64, 128, 4, 2, 2>(4));
+    t.push_back(make_config<128, 128, 128, 2, 4, 2>(4));
     return t;
   }();
   return table;

@@ -4,8 +4,13 @@
 //
 // Both are pure 16-bit permutations (bit-exact with the reference's transpose_c_hw indexing,
 // src/kernels/tensor_core_mma.cu:61-82,309-310) and HBM-bound: every element is read once and written once.
-//   * activations, channels >= 16: a 64(pixel) x 64(channel) tile goes through LDS; global reads are
-//     coalesced along pixels (128 B per wave-row), global writes are 16-byte vectors along channels.
+//   * activations, channels > 16, H*W % 4 == 0, x 8-byte aligned (the common case): pixels of all images are
+//     one flat index (b*HW + hw; a 4-pixel group never straddles two images). Each lane moves an 8-channel x
+//     4-pixel block: eight 8-byte loads along pixels (16 lanes read 128 contiguous bytes of one channel row),
+//     a register transpose, and four 16-byte NHWC stores (4 lanes write 64 contiguous bytes of one pixel).
+//     No LDS, no barrier.
+//   * activations, other channel counts > 16: a 64(pixel) x 64(channel) tile goes through LDS; global reads
+//     are coalesced along pixels (128 B per wave-row), global writes are 16-byte vectors along channels.
 //   * activations, channels < 16 (the 7x7 stem, C=3): one thread per pixel, C strided 2-byte reads that are
 //     coalesced across the wave, C_pad/8 16-byte writes.
 //   * weights: one thread per (o, tap, 8-channel chunk), 8 strided reads from a small L2-resident tensor and
@@ -25,15 +30,23 @@ struct ActJob {
   int batch, C, HW, Cp;
   int tiles_hw, tiles_c;  // tiled path
   int small;              // 1: one thread per pixel
+  int vec;                // 1: register-transpose path
+  long long vtiles_p;     // register-transpose path: 64-pixel tiles over batch*HW
+  int vtiles_c;           // ... and 128-channel tiles over Cp
 };
+
+constexpr int kVecPx = 64;   // pixels per register-transpose workgroup tile (16 lanes x 4 pixels)
+constexpr int kVecCh = 128;  // channels per tile (4 waves x 4 lanes x 8 channels)
 
 struct WJob {
   const uint16_t* __restrict__ w;
   uint16_t* __restrict__ wk;
   int O, C, RS, Cp;
+  int vec_load;  // 1: every filter starts 16-byte aligned
 };
 
 inline long long act_blocks(const ActJob& j) {
+  if (j.vec) return j.vtiles_p * j.vtiles_c;
   return j.small ? (static_cast<long long>(j.batch) * j.HW + kThreads - 1) / kThreads
                  : static_cast<long long>(j.tiles_hw) * j.tiles_c * j.batch;
 }
@@ -71,6 +84,33 @@ __device__ __forceinline__ void act_tiled(const ActJob& j, long long blk, uint16
         v[q] = uint32_t(tile[ch + 2 * q][hl]) | (uint32_t(tile[ch + 2 * q + 1][hl]) << 16);
       *reinterpret_cast<u32x4*>(dst + static_cast<long long>(hw) * j.Cp + c) = v;
     }
+  }
+}
+
+__device__ __forceinline__ void act_vec(const ActJob& j, long long blk) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const long long tp = blk % j.vtiles_p;
+  const int tc = int(blk / j.vtiles_p);
+  const long long P = tp * kVecPx + (lane & 15) * 4;           // first of this lane's 4 pixels (b*HW + hw)
+  const int c8 = tc * kVecCh + wave * 32 + (lane >> 4) * 8;    // first of its 8 channels
+  if (P >= static_cast<long long>(j.batch) * j.HW || c8 >= j.Cp) return;
+  const long long b = P / j.HW, hw = P - b * j.HW;
+  const uint16_t* src = j.x + (b * j.C + c8) * j.HW + hw;    // 8-byte aligned: HW % 4 == 0, hw % 4 == 0
+  u32x2 in[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    in[r] = c8 + r < j.C ? *reinterpret_cast<const u32x2*>(src + static_cast<long long>(r) * j.HW) : u32x2{0u, 0u};
+  uint16_t* dst = j.xn + P * j.Cp + c8;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // pixel q: channel pair (2d, 2d+1) -> dword d
+    u32x4 v;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t lo = in[2 * d][q >> 1], hi = in[2 * d + 1][q >> 1];
+      v[d] = (q & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    }
+    *reinterpret_cast<u32x4*>(dst + static_cast<long long>(q) * j.Cp) = v;
   }
 }
 
@@ -119,7 +159,12 @@ constexpr int kWElems = 8192;
 __device__ __forceinline__ void weight_filter(const WJob& j, long long o, uint16_t* buf) {
   const int n = j.C * j.RS;
   const uint16_t* src = j.w + o * n;
-  for (int i = threadIdx.x; i < n; i += kThreads) buf[i] = src[i];
+  if (j.vec_load) {  // filter rows start 16-byte aligned (w aligned, n % 8 == 0): 16-byte loads
+    for (int i = threadIdx.x * 8; i < n; i += kThreads * 8)
+      *reinterpret_cast<u32x4*>(buf + i) = *reinterpret_cast<const u32x4*>(src + i);
+  } else {
+    for (int i = threadIdx.x; i < n; i += kThreads) buf[i] = src[i];
+  }
   __syncthreads();
   const int cv = j.Cp / 8;
   uint16_t* dst = j.wk + o * static_cast<long long>(j.RS) * j.Cp;
@@ -148,21 +193,23 @@ __device__ __forceinline__ void weight_any(const WJob& j, long long blk, uint16_
 
 __global__ __launch_bounds__(kThreads) void repack_act_kernel(ActJob j) {
   __shared__ uint16_t tile[kTile][kTile + 2];
-  if (j.small) act_small(j, blockIdx.x);
+  if (j.vec) act_vec(j, blockIdx.x);
+  else if (j.small) act_small(j, blockIdx.x);
   else act_tiled(j, blockIdx.x, tile);
 }
 
 __global__ __launch_bounds__(kThreads) void repack_w_kernel(WJob j) {
-  __shared__ uint16_t buf[kWElems];
+  __shared__ __attribute__((aligned(16))) uint16_t buf[kWElems];
   weight_any(j, blockIdx.x, buf);
 }
 
 // Both repacks in one dispatch: blocks [0, n_act) repack activations, the rest repack weights.
 __global__ __launch_bounds__(kThreads) void repack_both_kernel(ActJob a, WJob w, long long n_act) {
-  __shared__ uint16_t buf[kWElems > kTile * (kTile + 2) ? kWElems : kTile * (kTile + 2)];
+  __shared__ __attribute__((aligned(16))) uint16_t buf[kWElems > kTile * (kTile + 2) ? kWElems : kTile * (kTile + 2)];
   const long long blk = blockIdx.x;
   if (blk < n_act) {
-    if (a.small) act_small(a, blk);
+    if (a.vec) act_vec(a, blk);
+    else if (a.small) act_small(a, blk);
     else act_tiled(a, blk, reinterpret_cast<uint16_t(*)[kTile + 2]>(buf));
   } else {
     weight_any(w, blk - n_act, buf);
@@ -182,6 +229,9 @@ int make_act(const void* x, void* xn, int batch, int C, int HW, int Cp, ActJob* 
   j->small = Cp <= 16 ? 1 : 0;
   j->tiles_hw = ceil_div_i(HW, kTile);
   j->tiles_c = ceil_div_i(Cp, kTile);
+  j->vec = (!j->small && HW % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 7u) == 0) ? 1 : 0;
+  j->vtiles_p = (static_cast<long long>(batch) * HW + kVecPx - 1) / kVecPx;
+  j->vtiles_c = ceil_div_i(Cp, kVecCh);
   return GIE_HIP_OK;
 }
 
@@ -193,6 +243,7 @@ int make_w(const void* w, void* wk, int O, int C, int RS, int Cp, WJob* j) {
   j->C = C;
   j->RS = RS;
   j->Cp = Cp;
+  j->vec_load = (aligned16(w) && (C * RS) % 8 == 0) ? 1 : 0;
   return GIE_HIP_OK;
 }
 

@@ -153,7 +153,7 @@ struct Fns {
   }
 };
 
-constexpr int kMaxEntries = 128;
+constexpr int kMaxEntries = 192;
 
 template <int... Is>
 struct FnTable {
