@@ -63,6 +63,11 @@ class GieConvGeom(ctypes.Structure):
         "pad_h", "pad_w", "out_h", "out_w", "c_pad", "relu")]
 
 
+class GieHaloConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "tile_n", "tile_k", "kernel_h", "kernel_w", "threads",
+                                            "version")]
+
+
 class GieIgemmConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "tile_m", "tile_n", "tile_k", "waves_m", "waves_n", "threads", "lds_bytes", "stages", "version")]
@@ -156,6 +161,10 @@ _HIP = {
     "gie_hip_igemm_config_get": ([_i, ctypes.POINTER(GieIgemmConfig)], _i),
     "gie_hip_igemm_occupancy": ([_i, _i, _ip], _i),
     "gie_hip_conv_igemm": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
+    "gie_hip_halo_config_count": ([], _i),
+    "gie_hip_halo_config_get": ([_i, ctypes.POINTER(GieHaloConfig)], _i),
+    "gie_hip_halo_check": ([_i, _GP, _ip], _i),
+    "gie_hip_conv_halo": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_splitk_reduce": ([_i, _vp, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _vp], _i),
     "gie_hip_reference_conv": ([_i, _GP, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_ceiling_mfma": ([_i, _i, _vp, _vp], _i),
@@ -751,6 +760,15 @@ class Graph:
 
 
 # ------------------------------------------------------------------------------------------------- kernels
+def halo_configs() -> list[dict]:
+    out = []
+    for i in range(hip().gie_hip_halo_config_count()):
+        c = GieHaloConfig()
+        check_hip(hip().gie_hip_halo_config_get(i, ctypes.byref(c)), "halo config")
+        out.append({f: getattr(c, f) for f, _ in c._fields_})
+    return out
+
+
 def igemm_configs() -> list[dict]:
     out = []
     for i in range(hip().gie_hip_igemm_config_count()):

@@ -13,6 +13,8 @@
  *   gie_hip_splitk_reduce            splitk_reduce<<<>>> launch            src/kernels/tensor_core_mma.cu:254-262,317-323
  *   gie_hip_igemm_config_*           the registered tile table             src/kernels/tensor_core_mma.cu:370-388
  *   gie_hip_igemm_occupancy          cudaOccupancyMaxActiveBlocksPerMultiprocessor in src/runtime/perf_model.cpp:75-102
+ *   gie_hip_conv_halo                tcmma_kernel<<<>>> launch (halo-tiled)  src/kernels/tensor_core_mma.cu:99-251,311-316
+ *   gie_hip_halo_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
  *   gie_hip_reference_conv           gpu_conv2d_reference                  src/runtime/reference.cu:31-91
  *   gie_hip_ceiling_*                ceilings microbenchmarks              src/profiling/ceilings.cu:21-58
  */
@@ -84,6 +86,31 @@ int gie_hip_igemm_occupancy(int index, int dtype, int* blocks_per_cu);
    bias may be null. partial must be 16-byte aligned and hold split*batch*out_channels*out_h*out_w floats. */
 int gie_hip_conv_igemm(int config, int dtype, const gie_conv_geom* g, const void* xn, const void* wk,
                        const void* bias, void* y, float* partial, int split, void* stream);
+
+/* One registered halo-tiled configuration: tile_m output channels x tile_n output pixels, channel slices of
+   tile_k, filter kernel_h x kernel_w. */
+typedef struct gie_halo_config {
+  int tile_m, tile_n, tile_k;
+  int kernel_h, kernel_w;
+  int threads;
+  int version;
+} gie_halo_config;
+
+int gie_hip_halo_config_count(void);
+int gie_hip_halo_config_get(int index, gie_halo_config* out);
+/* 0 when configuration `config` runs geometry g, with the LDS bytes per workgroup in *lds_bytes;
+   GIE_HIP_EUNSUPPORTED otherwise (other filter size, tile's input rows too large for the LDS stage, offsets
+   beyond 32 bits). */
+int gie_hip_halo_check(int config, const gie_conv_geom* g, int* lds_bytes);
+
+/* Halo-tiled implicit GEMM on MFMA 32x32x16 (FP32 accumulation) over the repacked buffers of
+   gie_hip_repack_act_and_w (xn [batch][in_h][in_w][c_pad], wk [out][kh*kw][c_pad], both 16-byte aligned): each
+   input pixel is staged once per 32-channel slice and read by every tap from LDS. split == 1:
+   y (NCHW, any 2-byte alignment) = round(relu?(acc + bias)), one rounding. split > 1:
+   partial[z][NCHW index] = FP32 sum over the z-th range of channel slices [floor(ns*z/split),
+   floor(ns*(z+1)/split)), ns = ceil(c_pad / tile_k); reduce with gie_hip_splitk_reduce. split <= ns. */
+int gie_hip_conv_halo(int config, int dtype, const gie_conv_geom* g, const void* xn, const void* wk,
+                      const void* bias, void* y, float* partial, int split, void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels])) */
 int gie_hip_splitk_reduce(int dtype, const float* partial, const void* bias, void* y, int64_t total, int split,

@@ -109,9 +109,18 @@ def test_plan_rejects_unsupported_precision():
 def test_forward_end_to_end_with_workspace_check():
     p = P(2, 8, 10, 10, 8, 3, 3, 1, 1, 1, 1)
     b = Bundle(p, 3, O.NORMAL)
-    opts = dict(backend="tensor_core")
+    # a kernel with a workspace (repack buffers) refuses a missing one
+    opts = dict(kernel=K16)
     ws = gie.DeviceBuffer(gie.workspace_size(p, **opts))
     expect_error("WorkspaceTooSmall", gie.forward, p, b.t, None, **opts)
+    b.t.poison()
+    gie.forward(p, b.t, ws, **opts)
+    gie.synchronize()
+    assert b.compare(b.t.y()).passed()
+    # whatever the dispatcher picks runs with exactly workspace_size() bytes (zero for the direct family)
+    opts = dict(backend="tensor_core")
+    need = gie.workspace_size(p, **opts)
+    ws = gie.DeviceBuffer(need) if need else None
     b.t.poison()
     gie.forward(p, b.t, ws, **opts)
     gie.synchronize()

@@ -180,11 +180,19 @@ def test_large_reduction_k4608_all_positive():
 
 def test_repeated_execution_is_stable():
     """tests/test_direct_conv.cpp:35-47 idea: repeated launches give bit-identical results (no LDS race)."""
-    p = problem(SHAPES[9], "fp16", True, True)
-    b = Bundle(p, 9)
-    for k in [k for k in kernels("fp16") if k.endswith("_sk1")][:3] + [k for k in kernels("fp16") if
-                                                                         k.endswith("_sk4")][:2]:
-        first, _ = run_plan(k, b)
-        for _ in range(3):
-            again, _ = run_plan(k, b, repeats=2)
-            assert np.array_equal(first.view(np.uint32), again.view(np.uint32)), k
+    for si in (9, 6):
+        p = problem(SHAPES[si], "fp16", True, True)
+        b = Bundle(p, 9)
+        ok = [k for k in kernels("fp16") if gie.kernel_supports(k, p)[0]]
+        for fam in ("halo_", "mfma_"):
+            picks = [k for k in ok if k.startswith(fam) and k.endswith("_sk1")][:3] + \
+                [k for k in ok if k.startswith(fam) and k.endswith("_sk4")][:2]
+            for k in picks:
+                _repeat_check(k, b)
+
+
+def _repeat_check(k, b):
+    first, _ = run_plan(k, b)
+    for _ in range(3):
+        again, _ = run_plan(k, b, repeats=2)
+        assert np.array_equal(first.view(np.uint32), again.view(np.uint32)), k
