@@ -1,10 +1,10 @@
 // The gfx950 halo-tiled MFMA family as registry entries (the role of the reference's tcmma registration,
-// src/kernels/tensor_core_mma.cu:264-395): the fused repack dispatch (X NCHW->NHWC, W OIHW->ORSC, channels
-// zero-padded to a multiple of 8), the halo-tiled implicit GEMM with the fused epilogue, and the split-K reduce
-// for split entries.
+// src/kernels/tensor_core_mma.cu:264-395): the channel-blocked repack dispatch (X and W in 32-channel slices,
+// zero-padded), the halo-tiled implicit GEMM with the fused epilogue, and the split-K reduce for split entries.
 //   * capability filter: fp16/bf16, a gfx950 device, the filter size of the entry, and the geometry checks of
 //     the kernel itself (the tile's input rows fit the LDS stage, 32-bit offsets) through gie_hip_halo_check;
-//   * workspace = [xn | 256-B align][wk | align][split * |Y| FP32 partials | align] (the MFMA family's layout).
+//   * workspace = [xb | 256-B align][wb | align][split * |Y| FP32 partials | align], xb/wb channel-blocked
+//     (32-channel slices, repack_blocked.hip).
 // Every launch goes through the kernel C-ABI (include/gie_hip.h); nothing here allocates or synchronizes.
 #include <hip/hip_runtime.h>
 
@@ -19,7 +19,7 @@ namespace gie {
 namespace {
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
-int c_pad_of(const ConvProblem& prob) { return (prob.p.in_channels + 7) / 8 * 8; }
+int c_pad_of(const ConvProblem& prob) { return (prob.p.in_channels + 31) / 32 * 32; }  // S slices of 32
 
 struct WsLayout {
   size_t xn_off, wk_off, part_off, total;
@@ -136,7 +136,7 @@ struct Fns {
     float* part = en.split > 1 ? reinterpret_cast<float*>(ws + l.part_off) : nullptr;
     void* s = la.stream;
     if (la.stage_events) GIE_HIP_CHECK(hipEventRecord(la.stage_events[0], la.stream));
-    check_kernel_status(gie_hip_repack_act_and_w(la.x, xn, la.w, wk, &g, s), "repack (NCHW->NHWC, OIHW->ORSC)");
+    check_kernel_status(gie_hip_repack_blocked(la.x, xn, la.w, wk, &g, s), "channel-blocked repack");
     if (la.stage_events) GIE_HIP_CHECK(hipEventRecord(la.stage_events[1], la.stream));
     check_kernel_status(gie_hip_conv_halo(en.config, dtype_of(prob.precision), &g, xn, wk, la.bias, la.y, part,
                                           en.split, s),
@@ -190,12 +190,13 @@ void register_halo_family(std::vector<KernelDesc>& out) {
     KernelDesc k;
     k.name = std::string("halo_") + to_string(en.precision) + "_" + std::to_string(en.info.kernel_h) + "x" +
              std::to_string(en.info.kernel_w) + "_" + std::to_string(en.info.tile_m) + "x" +
-             std::to_string(en.info.tile_n) + "x" + std::to_string(en.info.tile_k) + "_sk" +
-             std::to_string(en.split);
+             std::to_string(en.info.tile_n) + "x" + std::to_string(en.info.tile_k) + "_s" +
+             std::to_string(en.info.stages) + "_sk" + std::to_string(en.split);
     k.backend = Backend::kTensorCore;
     k.version = en.info.version;
     k.params = {{"block_m", en.info.tile_m}, {"block_n", en.info.tile_n}, {"block_k", en.info.tile_k},
-                {"kernel_h", en.info.kernel_h}, {"kernel_w", en.info.kernel_w}, {"split_k", en.split}};
+                {"kernel_h", en.info.kernel_h}, {"kernel_w", en.info.kernel_w}, {"stages", en.info.stages},
+                {"split_k", en.split}};
     k.threads_per_block = en.info.threads;
     k.tile_m = en.info.tile_m;
     k.tile_n = en.info.tile_n;

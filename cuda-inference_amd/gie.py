@@ -65,7 +65,7 @@ class GieConvGeom(ctypes.Structure):
 
 class GieHaloConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "tile_n", "tile_k", "kernel_h", "kernel_w", "threads",
-                                            "version")]
+                                            "stages", "version")]
 
 
 class GieIgemmConfig(ctypes.Structure):
@@ -161,6 +161,7 @@ _HIP = {
     "gie_hip_igemm_config_get": ([_i, ctypes.POINTER(GieIgemmConfig)], _i),
     "gie_hip_igemm_occupancy": ([_i, _i, _ip], _i),
     "gie_hip_conv_igemm": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
+    "gie_hip_repack_blocked": ([_vp, _vp, _vp, _vp, _GP, _vp], _i),
     "gie_hip_halo_config_count": ([], _i),
     "gie_hip_halo_config_get": ([_i, ctypes.POINTER(GieHaloConfig)], _i),
     "gie_hip_halo_check": ([_i, _GP, _ip], _i),

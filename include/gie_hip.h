@@ -13,6 +13,7 @@
  *   gie_hip_splitk_reduce            splitk_reduce<<<>>> launch            src/kernels/tensor_core_mma.cu:254-262,317-323
  *   gie_hip_igemm_config_*           the registered tile table             src/kernels/tensor_core_mma.cu:370-388
  *   gie_hip_igemm_occupancy          cudaOccupancyMaxActiveBlocksPerMultiprocessor in src/runtime/perf_model.cpp:75-102
+ *   gie_hip_repack_blocked           both launch_transpose calls, one launch src/kernels/tensor_core_mma.cu:78-82,309-310
  *   gie_hip_conv_halo                tcmma_kernel<<<>>> launch (halo-tiled)  src/kernels/tensor_core_mma.cu:99-251,311-316
  *   gie_hip_halo_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
  *   gie_hip_reference_conv           gpu_conv2d_reference                  src/runtime/reference.cu:31-91
@@ -93,6 +94,7 @@ typedef struct gie_halo_config {
   int tile_m, tile_n, tile_k;
   int kernel_h, kernel_w;
   int threads;
+  int stages; /* LDS stages of the load pipeline */
   int version;
 } gie_halo_config;
 
@@ -103,13 +105,17 @@ int gie_hip_halo_config_get(int index, gie_halo_config* out);
    beyond 32 bits). */
 int gie_hip_halo_check(int config, const gie_conv_geom* g, int* lds_bytes);
 
-/* Halo-tiled implicit GEMM on MFMA 32x32x16 (FP32 accumulation) over the repacked buffers of
-   gie_hip_repack_act_and_w (xn [batch][in_h][in_w][c_pad], wk [out][kh*kw][c_pad], both 16-byte aligned): each
-   input pixel is staged once per 32-channel slice and read by every tap from LDS. split == 1:
-   y (NCHW, any 2-byte alignment) = round(relu?(acc + bias)), one rounding. split > 1:
-   partial[z][NCHW index] = FP32 sum over the z-th range of channel slices [floor(ns*z/split),
-   floor(ns*(z+1)/split)), ns = ceil(c_pad / tile_k); reduce with gie_hip_splitk_reduce. split <= ns. */
-int gie_hip_conv_halo(int config, int dtype, const gie_conv_geom* g, const void* xn, const void* wk,
+/* Channel-blocked repack for the halo-tiled kernel, both tensors in one launch (S = ceil(in_channels / 32)):
+   xb[b][s][h*w][32] = x[b][32s + l][h*w] and wb[o][s][kh*kw][32] = w[o][32s + l][kh*kw] for channel 32s + l
+   < in_channels, 0 past it. x, w: caller tensors (any 2-byte alignment); xb, wb: 16-byte aligned. */
+int gie_hip_repack_blocked(const void* x, void* xb, const void* w, void* wb, const gie_conv_geom* g, void* stream);
+
+/* Halo-tiled implicit GEMM on MFMA 32x32x16 (FP32 accumulation) over the buffers of gie_hip_repack_blocked
+   (xb, wb 16-byte aligned; g->c_pad is ignored): each input pixel is staged once per 32-channel slice and read by
+   every tap from LDS. split == 1: y (NCHW, any 2-byte alignment) = round(relu?(acc + bias)), one rounding.
+   split > 1: partial[z][NCHW index] = FP32 sum over the z-th range of channel slices [floor(S*z/split),
+   floor(S*(z+1)/split)); reduce with gie_hip_splitk_reduce. split <= S. */
+int gie_hip_conv_halo(int config, int dtype, const gie_conv_geom* g, const void* xb, const void* wb,
                       const void* bias, void* y, float* partial, int split, void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels])) */
