@@ -247,30 +247,33 @@ int gie_plan_time_stages(void* plan, const void* x, const void* w, const void* b
     ExecutionPlan& pl = plan_of(plan);
     GIE_REQUIRE(iters > 0 && us3, StatusCode::kInvalidArgument, "bad iteration count");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // Every call gets its own four events and all calls are queued back to back (no host sync in between),
-    // so each stage interval is that kernel's time on the stream as it runs inside a steady stream of calls.
-    std::vector<hipEvent_t> ev(size_t(iters) * 4, nullptr);
+    // One full call fills the workspace; then each stage alone runs `iters` times back to back between two
+    // events (every stage is idempotent on a filled workspace), so us3[k] is that kernel's average duration
+    // inside a steady stream of its own launches. A stage the kernel does not have reads as ~0.
+    hipEvent_t e0 = nullptr, e1 = nullptr;
     struct G {
-      std::vector<hipEvent_t>& e;
+      hipEvent_t& a;
+      hipEvent_t& b;
       ~G() {
-        for (hipEvent_t x : e)
-          if (x) (void)hipEventDestroy(x);
+        if (a) (void)hipEventDestroy(a);
+        if (b) (void)hipEventDestroy(b);
       }
-    } guard{ev};
-    for (auto& e : ev) GIE_HIP_CHECK(hipEventCreate(&e));
-    pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s);  // warm
-    for (int it = 0; it < iters; ++it) pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, &ev[size_t(it) * 4]);
-    GIE_HIP_CHECK(hipEventSynchronize(ev.back()));
-    double acc[3] = {0, 0, 0};
-    for (int it = 0; it < iters; ++it) {
-      hipEvent_t* e = &ev[size_t(it) * 4];
-      for (int k = 0; k < 3; ++k) {
-        float ms = 0;
-        GIE_HIP_CHECK(hipEventElapsedTime(&ms, e[k], e[k + 1]));
-        acc[k] += ms * 1e3;
-      }
+    } guard{e0, e1};
+    GIE_HIP_CHECK(hipEventCreate(&e0));
+    GIE_HIP_CHECK(hipEventCreate(&e1));
+    pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s);
+    for (int k = 0; k < 3; ++k) {
+      pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, k);  // warm this stage
+      GIE_HIP_CHECK(hipEventRecord(e0, s));
+      for (int it = 0; it < iters; ++it) pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, k);
+      GIE_HIP_CHECK(hipEventRecord(e1, s));
+      GIE_HIP_CHECK(hipEventSynchronize(e1));
+      float ms = 0;
+      GIE_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+      us3[k] = ms * 1e3 / iters;
     }
-    for (int i = 0; i < 3; ++i) us3[i] = acc[i] / iters;
+    pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s);  // leave y as one full call made it
+    GIE_HIP_CHECK(hipStreamSynchronize(s));
   });
 }
 

@@ -80,7 +80,7 @@ ExecutionPlan::~ExecutionPlan() = default;
 
 void ExecutionPlan::execute(const ConstTensorRef& x, const ConstTensorRef& w, const ConstTensorRef* bias,
                             const TensorRef& y, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                            hipEvent_t* stage_events) const {
+                            int only_stage) const {
   const Conv2DParams& p = problem_.p;
   const DataType dt = problem_.dtype();
   check_tensor("input", x.data, x.dtype, x.shape, dt, p.input_shape());
@@ -117,11 +117,11 @@ void ExecutionPlan::execute(const ConstTensorRef& x, const ConstTensorRef& w, co
   if (cur != device_)
     throw Error(StatusCode::kInvalidArgument, "plan was created for device " + std::to_string(device_) +
                                                   " but device " + std::to_string(cur) + " is current");
-  execute_unchecked(x.data, w.data, bias_ptr, y.data, workspace, workspace_bytes, stream, stage_events);
+  execute_unchecked(x.data, w.data, bias_ptr, y.data, workspace, workspace_bytes, stream, only_stage);
 }
 
 void ExecutionPlan::execute_unchecked(const void* x, const void* w, const void* bias, void* y, void* workspace,
-                                      size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events) const {
+                                      size_t workspace_bytes, hipStream_t stream, int only_stage) const {
   RoctxRange range(kernel_->name.c_str());
   LaunchArgs la;
   la.problem = &problem_;
@@ -135,7 +135,7 @@ void ExecutionPlan::execute_unchecked(const void* x, const void* w, const void* 
   la.plan_data = lut_.data();
   la.plan_state = state_.get();
   la.stream = stream;
-  la.stage_events = stage_events;
+  la.only_stage = only_stage;
   kernel_->launch(la);
 }
 

@@ -135,20 +135,21 @@ struct Fns {
     void* wk = ws + l.wk_off;
     float* part = en.split > 1 ? reinterpret_cast<float*>(ws + l.part_off) : nullptr;
     void* s = la.stream;
-    if (la.stage_events) GIE_HIP_CHECK(hipEventRecord(la.stage_events[0], la.stream));
-    check_kernel_status(gie_hip_repack_blocked(la.x, xn, la.w, wk, &g, s), "channel-blocked repack");
-    if (la.stage_events) GIE_HIP_CHECK(hipEventRecord(la.stage_events[1], la.stream));
-    check_kernel_status(gie_hip_conv_halo(en.config, dtype_of(prob.precision), &g, xn, wk, la.bias, la.y, part,
+    const auto stage = [&](int k) { return la.only_stage < 0 || la.only_stage == k; };
+    if (stage(0)) {
+      check_kernel_status(gie_hip_repack_blocked(la.x, xn, la.w, wk, &g, s), "channel-blocked repack");
+    }
+    if (stage(1)) {
+      check_kernel_status(gie_hip_conv_halo(en.config, dtype_of(prob.precision), &g, xn, wk, la.bias, la.y, part,
                                           en.split, s),
                         "halo-tiled MFMA implicit GEMM");
-    if (la.stage_events) GIE_HIP_CHECK(hipEventRecord(la.stage_events[2], la.stream));
-    if (en.split > 1) {
+    }
+    if (en.split > 1 && stage(2)) {
       check_kernel_status(gie_hip_splitk_reduce(dtype_of(prob.precision), part, la.bias, la.y,
                                                 prob.p.output_shape().numel(), en.split, prob.p.out_channels,
                                                 g.out_h * g.out_w, g.relu, s),
                           "split-K reduce");
     }
-    if (la.stage_events) GIE_HIP_CHECK(hipEventRecord(la.stage_events[3], la.stream));
   }
 };
 

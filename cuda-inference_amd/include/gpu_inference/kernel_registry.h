@@ -34,9 +34,10 @@ struct LaunchArgs {
   const void* plan_data = nullptr;  // device-resident per-problem tables (see needs_lut)
   void* plan_state = nullptr;       // opaque per-plan state created by KernelDesc::create_state
   hipStream_t stream = nullptr;
-  // Optional profiling hooks: the MFMA family records events[0..3] = start, after the repack, after the
-  // implicit GEMM, after the split-K reduce (== after the GEMM when split == 1).
-  hipEvent_t* stage_events = nullptr;
+  // Profiling hook: >= 0 launches only that stage of a multi-launch kernel (0 = repack, 1 = main kernel,
+  // 2 = split-K reduce) on a workspace a full launch has already filled; every stage is idempotent, so
+  // back-to-back launches of one stage time that kernel alone. -1 (default) launches the whole chain.
+  int only_stage = -1;
 };
 
 struct KernelDesc {

@@ -72,8 +72,8 @@ int gie_plan_execute_unchecked(void* plan, const void* x, const void* w, const v
 int gie_plan_time(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
                   size_t workspace_bytes, void* stream, int warmup, int samples, double min_sample_ms,
                   double* stats7, int* inner);
-/* per-stage device time of one call, averaged over `iters` calls bracketed by stage events:
-   us3 = {repack, implicit GEMM, split-K reduce (0 when split == 1)} */
+/* per-stage device time: after one full call, each stage alone runs `iters` times back to back between two
+   events; us3 = average duration of {repack, implicit GEMM, split-K reduce (~0 when split == 1)} */
 int gie_plan_time_stages(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
                          size_t workspace_bytes, void* stream, int iters, double* us3);
 
