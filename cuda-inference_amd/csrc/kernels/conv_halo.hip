@@ -34,7 +34,7 @@
 #include <utility>
 #include <vector>
 
-#include "device_common.h"
+#include "lds_pipe.h"
 
 namespace gie_hip {
 namespace {
@@ -56,8 +56,6 @@ struct HaloGeom {
   float inv_ow, inv_oh, inv_hwo;  // reciprocals for the exact fast divisions below (operands < 2^22)
 };
 
-constexpr int kBufferWord3 = 0x00020000;
-constexpr int kOut = 0x80000000;  // buffer offset past any range: the load returns (writes) zeros
 constexpr int kSlotTable = 256;   // bytes at the start of LDS: slot -> pixel offset of (b, ih, 0), or -1
 constexpr int kMaxSlots = kSlotTable / 4;
 constexpr int kBiasBytes = 512;   // next: the workgroup's bias values as FP32 (tile_m <= 128)
@@ -81,56 +79,6 @@ struct HShape {
   static_assert(NST == 2 || NST == 3, "two or three LDS stages");
   static_assert(WU % 64 == 0, "weight region must be whole 1 KiB blocks");
 };
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
-// lgkmcnt[11:8], vmcnt[5:4] at [15:14])
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// n / d for 0 <= n < 2^22, d > 0, with inv = 1.0f / d: the float estimate is within 1 of the quotient, one
-// integer correction makes it exact (the host takes the exact path for larger pixel counts).
-__device__ __forceinline__ int fdiv(int n, int d, float inv) {
-  int q = int(float(n) * inv);
-  const int r = n - q * d;
-  q += (r >= d ? 1 : 0) - (r < 0 ? 1 : 0);
-  return q;
-}
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-// Buffer resource (V#) of a raw byte buffer: base, stride 0, num_records = bytes, word 3 as above. Offsets at or
-// past num_records read as zeros.
-__device__ __forceinline__ v4i make_vsharp(const void* base, int bytes) {
-  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-  return v4i{int(unsigned(a)), int(unsigned(a >> 32) & 0xffffu), bytes, kBufferWord3};
-}
-
-// 16 bytes per lane straight into LDS at lds_base + 16 * lane (buffer_load_dwordx4 ... lds; M0 = LDS byte
-// address). Issued through inline assembly so the compiler neither waits on it at every later LDS access nor
-// reorders it: the kernel counts these loads itself (wait_vmcnt) and fences them with barriers.
-__device__ __forceinline__ void dma16(v4i rsrc, unsigned lds_base, int voff) {
-  // lds_base is wave-uniform by construction; readfirstlane states it for the compiler (M0 is a scalar)
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(
-                   __builtin_amdgcn_readfirstlane(lds_base)),
-               "v"(voff), "s"(rsrc)
-               : "m0");
-}
-
-// Workgroup barrier for the load pipeline. __syncthreads() also emits a release fence, which the compiler
-// lowers to s_waitcnt vmcnt(0): that would wait for every prefetch in flight. Here the caller has already waited
-// for exactly the loads that must have landed (wait_vmcnt); this barrier only drains this wave's LDS reads and
-// orders the waves. The memory clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void stage_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
-  asm volatile("s_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ unsigned lds_addr(const unsigned char* p) {
-  return unsigned(reinterpret_cast<size_t>((__attribute__((address_space(3))) const unsigned char*)p));
-}
 
 template <typename E, int KH, int KW, int TO, int TPX, int NST, int KBA>
 __global__ __launch_bounds__(TPX / 64 * KH * 2 * 64) void halo_kernel(
@@ -508,8 +456,6 @@ const std::vector<HaloConfig>& halo_configs() {
   return t;
 }
 
-constexpr int kLdsLimit = 160 * 1024;
-
 // Geometry checks shared by the capability query and the launch. Fills g, the LDS bytes and the number of
 // load instructions per wave per slice on success.
 int halo_prepare(const HaloConfig& c, const gie_conv_geom* gg, HaloGeom* g, int* lds_bytes, int* kb) {
@@ -575,22 +521,6 @@ int halo_prepare(const HaloConfig& c, const gie_conv_geom* gg, HaloGeom* g, int*
   return GIE_HIP_OK;
 }
 
-int set_lds_limit(HaloFn fn, int bytes) {
-  if (bytes <= 64 * 1024) return GIE_HIP_OK;
-  static std::mutex mu;
-  static std::set<std::pair<const void*, int>> done;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return int(hipErrorInvalidDevice);
-  std::lock_guard<std::mutex> lock(mu);
-  if (done.count({reinterpret_cast<const void*>(fn), dev})) return GIE_HIP_OK;
-  // the largest amount any geometry may use, so one attribute call covers them all
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  if (e != hipSuccess) return int(e);
-  done.insert({reinterpret_cast<const void*>(fn), dev});
-  return GIE_HIP_OK;
-}
-
 }  // namespace
 }  // namespace gie_hip
 
@@ -639,7 +569,7 @@ extern "C" int gie_hip_conv_halo(int config, int dtype, const gie_conv_geom* gg,
   g.span = int(span);
   HaloFn fn = c.fn[dtype == GIE_HIP_BF16 ? 1 : 0][kb];
   if (!fn) return GIE_HIP_EUNSUPPORTED;
-  if (int rc = set_lds_limit(fn, lds)) return rc;
+  if (int rc = set_lds_limit(reinterpret_cast<const void*>(fn), lds)) return rc;
   hipLaunchKernelGGL(fn, dim3(unsigned(n_ot * n_pt), 1, unsigned(split)), dim3(c.info.threads), lds,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(xn),
                      static_cast<const uint16_t*>(wk), static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),

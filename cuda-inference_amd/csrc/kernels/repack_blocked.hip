@@ -112,9 +112,11 @@ __global__ __launch_bounds__(kThreads) void repack_blocked_kernel(BlockedJob j) 
 
 using namespace gie_hip;
 
-extern "C" int gie_hip_repack_blocked(const void* x, void* xb, const void* w, void* wb, const gie_conv_geom* g,
-                                      void* stream) {
-  if (!g || !x || !xb || !w || !wb) return GIE_HIP_EINVAL;
+namespace {
+
+// x == nullptr: weights only (n_act = 0)
+int repack_blocked(const void* x, void* xb, const void* w, void* wb, const gie_conv_geom* g, void* stream) {
+  if (!g || !w || !wb || (x && !xb)) return GIE_HIP_EINVAL;
   if ((reinterpret_cast<uintptr_t>(xb) & 15u) || (reinterpret_cast<uintptr_t>(wb) & 15u)) return GIE_HIP_EINVAL;
   if ((reinterpret_cast<uintptr_t>(x) & 1u) || (reinterpret_cast<uintptr_t>(w) & 1u)) return GIE_HIP_EINVAL;
   BlockedJob j;
@@ -134,8 +136,8 @@ extern "C" int gie_hip_repack_blocked(const void* x, void* xb, const void* w, vo
   j.RS = int(rs);
   j.S = (j.C + 31) / 32;
   j.n_pt = int((hw + kTilePx - 1) / kTilePx);
-  j.n_act = static_cast<long long>(j.B) * j.S * j.n_pt;
-  j.xvec = (hw % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 7u) == 0) ? 1 : 0;
+  j.n_act = x ? static_cast<long long>(j.B) * j.S * j.n_pt : 0;
+  j.xvec = (x && hw % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 7u) == 0) ? 1 : 0;
   j.wlds = (rs * j.C <= kWBuf) ? 1 : 0;
   j.wvec = ((reinterpret_cast<uintptr_t>(w) & 15u) == 0 && (rs * j.C) % 8 == 0) ? 1 : 0;
   const long long blocks = j.n_act + j.O;
@@ -144,4 +146,16 @@ extern "C" int gie_hip_repack_blocked(const void* x, void* xb, const void* w, vo
                      static_cast<hipStream_t>(stream), j);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GIE_HIP_OK : int(e);
+}
+
+}  // namespace
+
+extern "C" int gie_hip_repack_blocked(const void* x, void* xb, const void* w, void* wb, const gie_conv_geom* g,
+                                      void* stream) {
+  if (!x) return GIE_HIP_EINVAL;
+  return repack_blocked(x, xb, w, wb, g, stream);
+}
+
+extern "C" int gie_hip_repack_w_blocked(const void* w, void* wb, const gie_conv_geom* g, void* stream) {
+  return repack_blocked(nullptr, nullptr, w, wb, g, stream);
 }

@@ -9,6 +9,7 @@ namespace gie {
 
 void register_mfma_family(std::vector<KernelDesc>& out);  // mfma_family.cpp
 void register_halo_family(std::vector<KernelDesc>& out);  // halo_family.cpp
+void register_band_family(std::vector<KernelDesc>& out);  // band_family.cpp
 
 std::string KernelDesc::describe() const {
   std::ostringstream os;
@@ -23,6 +24,7 @@ std::vector<KernelDesc>& registry_storage() {
   static std::vector<KernelDesc> registry = [] {
     std::vector<KernelDesc> r;
     r.reserve(1024);  // stable element addresses even if tests inject extra entries
+    register_band_family(r);
     register_halo_family(r);
     register_mfma_family(r);
     std::set<std::string> names;

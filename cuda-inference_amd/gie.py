@@ -68,6 +68,11 @@ class GieHaloConfig(ctypes.Structure):
                                             "stages", "version")]
 
 
+class GieBandConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "tile_n", "tile_k", "kernel_h", "kernel_w", "threads",
+                                            "stages", "version")]
+
+
 class GieIgemmConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "tile_m", "tile_n", "tile_k", "waves_m", "waves_n", "threads", "lds_bytes", "stages", "version")]
@@ -166,6 +171,11 @@ _HIP = {
     "gie_hip_halo_config_get": ([_i, ctypes.POINTER(GieHaloConfig)], _i),
     "gie_hip_halo_check": ([_i, _GP, _ip], _i),
     "gie_hip_conv_halo": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
+    "gie_hip_repack_w_blocked": ([_vp, _vp, _GP, _vp], _i),
+    "gie_hip_band_config_count": ([], _i),
+    "gie_hip_band_config_get": ([_i, ctypes.POINTER(GieBandConfig)], _i),
+    "gie_hip_band_check": ([_i, _GP, _ip], _i),
+    "gie_hip_conv_band": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_splitk_reduce": ([_i, _vp, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _vp], _i),
     "gie_hip_reference_conv": ([_i, _GP, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_ceiling_mfma": ([_i, _i, _vp, _vp], _i),
@@ -766,6 +776,15 @@ def halo_configs() -> list[dict]:
     for i in range(hip().gie_hip_halo_config_count()):
         c = GieHaloConfig()
         check_hip(hip().gie_hip_halo_config_get(i, ctypes.byref(c)), "halo config")
+        out.append({f: getattr(c, f) for f, _ in c._fields_})
+    return out
+
+
+def band_configs() -> list[dict]:
+    out = []
+    for i in range(hip().gie_hip_band_config_count()):
+        c = GieBandConfig()
+        check_hip(hip().gie_hip_band_config_get(i, ctypes.byref(c)), "band config")
         out.append({f: getattr(c, f) for f, _ in c._fields_})
     return out
 

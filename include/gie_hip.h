@@ -16,6 +16,10 @@
  *   gie_hip_repack_blocked           both launch_transpose calls, one launch src/kernels/tensor_core_mma.cu:78-82,309-310
  *   gie_hip_conv_halo                tcmma_kernel<<<>>> launch (halo-tiled)  src/kernels/tensor_core_mma.cu:99-251,311-316
  *   gie_hip_halo_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
+ *   gie_hip_repack_w_blocked         launch_transpose(w, wk, O, C, KH*KW)  src/kernels/tensor_core_mma.cu:78-82,310
+ *   gie_hip_conv_band                transpose_c_hw of x + tcmma_kernel, fused (no activation repack)
+ *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309
+ *   gie_hip_band_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
  *   gie_hip_reference_conv           gpu_conv2d_reference                  src/runtime/reference.cu:31-91
  *   gie_hip_ceiling_*                ceilings microbenchmarks              src/profiling/ceilings.cu:21-58
  */
@@ -116,6 +120,35 @@ int gie_hip_repack_blocked(const void* x, void* xb, const void* w, void* wb, con
    split > 1: partial[z][NCHW index] = FP32 sum over the z-th range of channel slices [floor(S*z/split),
    floor(S*(z+1)/split)); reduce with gie_hip_splitk_reduce. split <= S. */
 int gie_hip_conv_halo(int config, int dtype, const gie_conv_geom* g, const void* xb, const void* wb,
+                      const void* bias, void* y, float* partial, int split, void* stream);
+
+/* Weights only of gie_hip_repack_blocked: wb[o][s][kh*kw][32] = w[o][32s + l][kh*kw], zero past in_channels
+   (w any 2-byte alignment, wb 16-byte aligned). Feeds gie_hip_conv_band, which reads activations as NCHW. */
+int gie_hip_repack_w_blocked(const void* w, void* wb, const gie_conv_geom* g, void* stream);
+
+/* One registered band configuration: tile_m (32) output channels x tile_n padded output pixels (one band of
+   rows of one image), channel slices of tile_k, filter kernel_h x kernel_w. */
+typedef struct gie_band_config {
+  int tile_m, tile_n, tile_k;
+  int kernel_h, kernel_w;
+  int threads;
+  int stages; /* LDS stages of the weight pipeline */
+  int version;
+} gie_band_config;
+
+int gie_hip_band_config_count(void);
+int gie_hip_band_config_get(int index, gie_band_config* out);
+/* 0 when configuration `config` runs geometry g, with the LDS bytes per workgroup in *lds_bytes;
+   GIE_HIP_EUNSUPPORTED otherwise (other filter size, band rows too wide for the LDS stage, offsets beyond
+   32 bits). */
+int gie_hip_band_check(int config, const gie_conv_geom* g, int* lds_bytes);
+
+/* Band convolution on MFMA 32x32x16 (FP32 accumulation) reading x as NCHW directly (any 2-byte alignment;
+   8-byte loads when x is 8-byte aligned and every band's rows start on a 4-pixel boundary) and the weights from
+   gie_hip_repack_w_blocked (wb 16-byte aligned; g->c_pad is ignored). split == 1: y (NCHW, any 2-byte alignment)
+   = round(relu?(acc + bias)), one rounding. split > 1: partial[z][NCHW index] = FP32 sum over channel slices
+   [floor(S*z/split), floor(S*(z+1)/split)); reduce with gie_hip_splitk_reduce. split <= S. */
+int gie_hip_conv_band(int config, int dtype, const gie_conv_geom* g, const void* x, const void* wb,
                       const void* bias, void* y, float* partial, int split, void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels])) */

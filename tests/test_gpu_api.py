@@ -317,10 +317,12 @@ def _poison_async(b: Bundle, stream):
     gie.check_hip(gie.hip().gie_hip_fill_u16(b.t.dy.addr, b.t.ny, 0xFFFF, stream.h), "fill")
 
 
-@pytest.mark.parametrize("kernel", [K16, K16_SK4, "mfma_bf16_64x64x32_w2x2_s4_sk2"])
+@pytest.mark.parametrize("kernel", [K16, K16_SK4, "mfma_bf16_64x64x32_w2x2_s4_sk2", "band_fp16_3x3_32x224x32_s4_sk1",
+                                    "band_bf16_3x3_32x224x32_s4_sk2"])
 def test_graph_replay_with_changing_inputs(kernel):
     prec = "bf16" if "bf16" in kernel else "fp16"
-    p = P(2, 32, 14, 14, 48, 3, 3, 1, 1, 1, 1, precision=prec)
+    c = 128 if kernel.startswith("band_") else 32  # four 32-channel slices: enough K for the band kernel's split
+    p = P(2, c, 14, 14, 48, 3, 3, 1, 1, 1, 1, precision=prec)
     plan = gie.Plan(p, kernel)  # plans exist before capture
     ws = gie.DeviceBuffer(plan.workspace_bytes)
     bufs = Bundle(p, 1)

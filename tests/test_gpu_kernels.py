@@ -184,7 +184,7 @@ def test_repeated_execution_is_stable():
         p = problem(SHAPES[si], "fp16", True, True)
         b = Bundle(p, 9)
         ok = [k for k in kernels("fp16") if gie.kernel_supports(k, p)[0]]
-        for fam in ("halo_", "mfma_"):
+        for fam in ("band_", "halo_", "mfma_"):
             picks = [k for k in ok if k.startswith(fam) and k.endswith("_sk1")][:3] + \
                 [k for k in ok if k.startswith(fam) and k.endswith("_sk4")][:2]
             for k in picks:
