@@ -10,6 +10,7 @@ namespace gie {
 void register_mfma_family(std::vector<KernelDesc>& out);  // mfma_family.cpp
 void register_halo_family(std::vector<KernelDesc>& out);  // halo_family.cpp
 void register_band_family(std::vector<KernelDesc>& out);  // band_family.cpp
+void register_pw_family(std::vector<KernelDesc>& out);    // pw_family.cpp
 
 std::string KernelDesc::describe() const {
   std::ostringstream os;
@@ -27,6 +28,7 @@ std::vector<KernelDesc>& registry_storage() {
     register_band_family(r);
     register_halo_family(r);
     register_mfma_family(r);
+    register_pw_family(r);  // after mfma: its unaligned-pointer fallback is an mfma entry
     std::set<std::string> names;
     for (const auto& k : r) {
       if (!names.insert(k.name).second) throw Error(StatusCode::kInternal, "duplicate kernel name " + k.name);

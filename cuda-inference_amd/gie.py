@@ -176,6 +176,8 @@ _HIP = {
     "gie_hip_band_config_get": ([_i, ctypes.POINTER(GieBandConfig)], _i),
     "gie_hip_band_check": ([_i, _GP, _ip], _i),
     "gie_hip_conv_band": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
+    "gie_hip_pw_check": ([_GP, _ip], _i),
+    "gie_hip_conv_pw": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_splitk_reduce": ([_i, _vp, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _vp], _i),
     "gie_hip_reference_conv": ([_i, _GP, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_ceiling_mfma": ([_i, _i, _vp, _vp], _i),

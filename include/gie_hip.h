@@ -20,6 +20,8 @@
  *   gie_hip_conv_band                transpose_c_hw of x + tcmma_kernel, fused (no activation repack)
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309
  *   gie_hip_band_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
+ *   gie_hip_conv_pw, gie_hip_pw_check both transposes + tcmma_kernel for 1x1 filters, fused (no repack)
+ *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
  *   gie_hip_reference_conv           gpu_conv2d_reference                  src/runtime/reference.cu:31-91
  *   gie_hip_ceiling_*                ceilings microbenchmarks              src/profiling/ceilings.cu:21-58
  */
@@ -150,6 +152,16 @@ int gie_hip_band_check(int config, const gie_conv_geom* g, int* lds_bytes);
    [floor(S*z/split), floor(S*(z+1)/split)); reduce with gie_hip_splitk_reduce. split <= S. */
 int gie_hip_conv_band(int config, int dtype, const gie_conv_geom* g, const void* x, const void* wb,
                       const void* bias, void* y, float* partial, int split, void* stream);
+
+/* 0 when the pointwise kernel runs geometry g (1x1 filter, stride 1, no padding, in_channels % 8 == 0,
+   in_h*in_w % 8 == 0, offsets within 32 bits), with its LDS bytes per workgroup in *lds_bytes. */
+int gie_hip_pw_check(const gie_conv_geom* g, int* lds_bytes);
+
+/* Pointwise convolution on MFMA 32x32x16 (FP32 accumulation) straight from the caller's tensors: x NCHW,
+   w [out_channels][in_channels], y NCHW, all 16-byte aligned (GIE_HIP_EUNSUPPORTED otherwise), bias any 2-byte
+   alignment or NULL. y = round(relu?(acc + bias)), one rounding. One launch, no workspace. */
+int gie_hip_conv_pw(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
+                    void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels])) */
 int gie_hip_splitk_reduce(int dtype, const float* partial, const void* bias, void* y, int64_t total, int split,
