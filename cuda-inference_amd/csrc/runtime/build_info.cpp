@@ -1,6 +1,8 @@
 // Build provenance; the GIE_* macros are defined by the library's Makefile.
 #include "gpu_inference/build_info.h"
 
+#include <string>
+
 #ifndef GIE_SOURCE_FINGERPRINT
 #define GIE_SOURCE_FINGERPRINT "unknown"
 #endif
@@ -26,7 +28,13 @@ const BuildInfo& build_info() {
     b.build_type = GIE_BUILD_TYPE;
     b.offload_archs = GIE_OFFLOAD_ARCHS;
     b.hipcc_version = GIE_HIPCC_VERSION;
-    b.cxx_compiler = "hipcc";
+#if defined(__clang__)
+    b.cxx_compiler = std::string("clang ") + __clang_version__;
+#elif defined(__GNUC__)
+    b.cxx_compiler = std::string("g++ ") + __VERSION__;
+#else
+    b.cxx_compiler = "unknown";
+#endif
     b.hip_flags = GIE_HIP_FLAGS_STR;
 #ifdef GIE_HAS_ROCTX
     b.has_roctx = true;

@@ -62,10 +62,8 @@ float draw(Rng& rng, Distribution d) {
 }
 }  // namespace
 
-ConvData make_conv_data(const ConvProblem& prob, uint64_t seed, Distribution dist, Scaling scaling) {
+HostConvData make_host_conv_data(const ConvProblem& prob, uint64_t seed, Distribution dist, Scaling scaling) {
   validate_problem(prob);
-  ConvData d;
-  d.prob = prob;
   const Conv2DParams& p = prob.p;
   Rng rng(seed);
   std::vector<float> rx(size_t(p.input_shape().numel())), rw(size_t(p.weight_shape().numel())),
@@ -77,21 +75,36 @@ ConvData make_conv_data(const ConvProblem& prob, uint64_t seed, Distribution dis
   const float blim = scaling == Scaling::kBenchmark ? 0.1f : 1.0f;
   for (auto& v : rb) v = rng.uniform(-blim, blim);
 
-  const DataType dt = prob.dtype();
-  const bool half_storage = dt != DataType::kFloat32;
-  d.hx.resize(rx.size());
-  d.hw.resize(rw.size());
-  d.hb.resize(rb.size());
-  for (size_t i = 0; i < rx.size(); ++i) d.hx[i] = quantize_to(prob.precision, rx[i]);
-  for (size_t i = 0; i < rw.size(); ++i) d.hw[i] = quantize_to(prob.precision, rw[i]);
-  for (size_t i = 0; i < rb.size(); ++i) d.hb[i] = half_storage ? quantize_to(prob.precision, rb[i]) : rb[i];
+  HostConvData h;
+  const bool half_storage = prob.dtype() != DataType::kFloat32;
+  h.hx.resize(rx.size());
+  h.hw.resize(rw.size());
+  h.hb.resize(rb.size());
+  for (size_t i = 0; i < rx.size(); ++i) h.hx[i] = quantize_to(prob.precision, rx[i]);
+  for (size_t i = 0; i < rw.size(); ++i) h.hw[i] = quantize_to(prob.precision, rw[i]);
+  for (size_t i = 0; i < rb.size(); ++i) h.hb[i] = half_storage ? quantize_to(prob.precision, rb[i]) : rb[i];
+  if (prob.precision == Precision::kTf32) {
+    h.raw_x = std::move(rx);
+    h.raw_w = std::move(rw);
+  }
+  return h;
+}
 
-  d.dx = upload_as(prob.precision == Precision::kTf32 ? rx : d.hx, dt);
-  d.dw = upload_as(prob.precision == Precision::kTf32 ? rw : d.hw, dt);
-  d.db = upload_as(d.hb, dt);
-  d.dy = DeviceBuffer(size_t(p.output_shape().numel()) * dtype_size(dt));
+ConvData make_conv_data(const ConvProblem& prob, uint64_t seed, Distribution dist, Scaling scaling) {
+  HostConvData h = make_host_conv_data(prob, seed, dist, scaling);
+  ConvData d;
+  d.prob = prob;
+  const DataType dt = prob.dtype();
+  const bool tf32 = prob.precision == Precision::kTf32;
+  d.dx = upload_as(tf32 ? h.raw_x : h.hx, dt);
+  d.dw = upload_as(tf32 ? h.raw_w : h.hw, dt);
+  d.db = upload_as(h.hb, dt);
+  d.dy = DeviceBuffer(size_t(prob.p.output_shape().numel()) * dtype_size(dt));
   GIE_HIP_CHECK(hipMemset(d.dy.data(), 0xFF, d.dy.size()));  // NaN bits: unwritten outputs fail comparisons
   GIE_HIP_CHECK(hipDeviceSynchronize());
+  d.hx = std::move(h.hx);
+  d.hw = std::move(h.hw);
+  d.hb = std::move(h.hb);
   return d;
 }
 

@@ -179,6 +179,7 @@ _HIP = {
     "gie_hip_pw_check": ([_GP, _ip], _i),
     "gie_hip_conv_pw": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_splitk_reduce": ([_i, _vp, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _vp], _i),
+    "gie_hip_bias_act": ([_i, _vp, _vp, ctypes.c_int64, _i, _i, _i, _vp], _i),
     "gie_hip_reference_conv": ([_i, _GP, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_ceiling_mfma": ([_i, _i, _vp, _vp], _i),
     "gie_hip_ceiling_copy": ([_vp, _vp, _sz, _vp], _i),

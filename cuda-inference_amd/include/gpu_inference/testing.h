@@ -42,6 +42,15 @@ struct ConvData {
   TensorRef y_ref();
 };
 
+// The seeded values of make_conv_data with no device work (same draw order and quantization): what the
+// reference consumes, and for kTf32 the unrounded FP32 values the device receives (raw_x, raw_w; empty otherwise).
+struct HostConvData {
+  std::vector<float> hx, hw, hb;
+  std::vector<float> raw_x, raw_w;
+};
+HostConvData make_host_conv_data(const ConvProblem& prob, uint64_t seed, Distribution dist = Distribution::kUniform,
+                                 Scaling scaling = Scaling::kReference);
+
 ConvData make_conv_data(const ConvProblem& prob, uint64_t seed, Distribution dist = Distribution::kUniform,
                         Scaling scaling = Scaling::kReference);
 DeviceBuffer upload_as(const std::vector<float>& v, DataType dt);

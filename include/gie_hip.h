@@ -22,6 +22,7 @@
  *   gie_hip_band_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
  *   gie_hip_conv_pw, gie_hip_pw_check both transposes + tcmma_kernel for 1x1 filters, fused (no repack)
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
+ *   gie_hip_bias_act                 launch_bias_act / _bias_add / _relu   src/kernels/elementwise.cu:13-56
  *   gie_hip_reference_conv           gpu_conv2d_reference                  src/runtime/reference.cu:31-91
  *   gie_hip_ceiling_*                ceilings microbenchmarks              src/profiling/ceilings.cu:21-58
  */
@@ -166,6 +167,12 @@ int gie_hip_conv_pw(int dtype, const gie_conv_geom* g, const void* x, const void
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels])) */
 int gie_hip_splitk_reduce(int dtype, const float* partial, const void* bias, void* y, int64_t total, int split,
                           int out_channels, int hw_out, int relu, void* stream);
+
+/* Stand-alone epilogue pass over an NCHW output, in place (the unfused side of the fusion experiment):
+   y[i] = round(relu?(f32(y[i]) + f32(bias[(i / hw_out) % out_channels]))); bias may be NULL (ReLU only). dtype
+   GIE_HIP_FP32, _FP16 or _BF16; y and bias aligned to their element size. No-op when bias is NULL and relu 0. */
+int gie_hip_bias_act(int dtype, void* y, const void* bias, int64_t total, int out_channels, int hw_out, int relu,
+                     void* stream);
 
 /* Double-accumulation direct convolution (validation reference for the autotuner and tests):
    y_ref, scale: float[batch*out_channels*out_h*out_w]. dtype may be GIE_HIP_FP32 here. */

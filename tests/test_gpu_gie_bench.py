@@ -1,0 +1,82 @@
+"""The gie_bench harness on the GPU: every row type of the reference's benchmarks/benchmark_main.cpp flow.
+
+Two small workloads (a 3x3 and a 1x1 layer) at fp16, bf16 and fp32 through tensor_core (fixed and tuned
+configurations), the dispatcher, a kernel named on the command line, the CPU reference and the copy rows, fused
+and unfused. Checks that each FP16/BF16 GPU row validated against the double reference before it was timed and
+carries positive timings, that the unfused rows (convolution + stand-alone bias and ReLU passes) validate under
+the two-rounding tolerance, that FP32 rows say 'unsupported' (no FP32 MFMA family is registered), and that the
+dispatcher row records its selection and the warm host overhead.
+"""
+import json
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "cuda-inference_amd", "lib", "gie_bench")
+
+pytestmark = pytest.mark.gpu
+
+
+def test_gie_bench_rows_on_gpu(tmp_path):
+    doc = {"split": "gpu_test", "workloads": [
+        {"name": "l3x3", "category": "t", "B": 2, "C": 64, "H": 14, "O": 64, "K": 3, "P": 1},
+        {"name": "l1x1", "category": "t", "B": 2, "C": 64, "H": 16, "O": 96, "K": 1, "relu": False},
+    ]}
+    wl = tmp_path / "w.json"
+    wl.write_text(json.dumps(doc))
+    out = tmp_path / "res"
+    named = "mfma_fp16_64x64x64_w2x2_s4_sk1"
+    cmd = [BIN, "--workloads", str(wl), "--backends", "tensor_core,dispatcher,cpu_reference,simt_tiled",
+           "--precisions", "fp16,bf16,fp32", "--mode", "both", "--fusion", "both", "--kernels", named,
+           "--warmup", "1", "--samples", "3", "--min-sample-ms", "0.2", "--tune-samples", "2", "--model-keep", "3",
+           "--cache", str(tmp_path / "tune.json"), "--e2e", "--out", str(out), "--tag", "gpu"]
+    print(" ".join(cmd), flush=True)
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    print(p.stderr[-3000:], flush=True)
+    assert p.returncode == 0, p.stderr[-2000:]
+    rows = [json.loads(line) for line in open(out / "results.jsonl")]
+    by = {}
+    for r in rows:
+        by.setdefault((r["workload"], r["precision"], r["backend"], r["fusion"], r["mode"]), []).append(r)
+
+    for w in ("l3x3", "l1x1"):
+        for prec in ("fp16", "bf16"):
+            for mode in ("fixed", "tuned"):
+                for fusion in ("fused", "unfused"):
+                    (r,) = by[(w, prec, "tensor_core", fusion, mode)]
+                    assert r["status"] == "ok", r
+                    assert r["validated"] is True and r["nan_count"] == 0 and r["frac_over_tol"] == 0
+                    assert r["median_us"] > 0 and r["tflops"] > 0 and r["samples"] == 3
+                    if mode == "fixed":
+                        assert r["kernel"].startswith(f"mfma_{prec}_128x128x64_w4x2_s3_sk1"), r["kernel"]
+                    assert ("+bias+relu(unfused)" in r["kernel"]) == (fusion == "unfused")
+                    assert r["host_sync_latency_us"] > 0
+            (t,) = by[(w, prec, "tensor_core", "fused", "tuned")]
+            assert "tuning_seconds" in t and "tuning_cache_hit" in t
+            (d,) = by[(w, prec, "dispatcher", "fused", "auto")]
+            assert d["status"] == "ok", d
+            assert d["config"].startswith("selected ") and d["warm_dispatch_overhead_us"] == pytest.approx(
+                d["dispatch_api_host_us"] - d["raw_launch_host_us"])
+            (k,) = by[(w, prec, "kernel", "fused", "named")]
+            if prec == "fp16":
+                assert k["status"] == "ok" and k["kernel"] == named, k
+            else:
+                assert k["status"] == "unsupported" and "fp16" in k["reason"], k
+            (c,) = by[(w, prec, "cpu_reference", "fused", "host")]
+            assert c["status"] == "ok" and c["max_abs_err"] < 1e-5, c
+            (s,) = by[(w, prec, "simt_tiled", "fused", "n/a")]
+            assert s["status"] == "unsupported"
+            (m,) = by[(w, prec, "memcpy", "n/a", "pinned")]
+            assert m["status"] == "ok" and m["h2d_us"] > 0 and m["d2h_us"] > 0
+        for mode in ("fixed", "tuned"):
+            (f,) = by[(w, "fp32", "tensor_core", "fused", mode)]
+            assert f["status"] == "unsupported", f
+        (fd,) = by[(w, "fp32", "dispatcher", "fused", "auto")]
+        assert fd["status"] == "unsupported", fd
+    # the 3x3 fixed configuration is a two-launch kernel (repack + convolution): both stages are timed
+    (r,) = by[("l3x3", "fp16", "tensor_core", "fused", "fixed")]
+    assert r["stage_repack_us"] > 0 and r["stage_conv_us"] > 0 and "stage_reduce_us" not in r
+    meta = json.load(open(out / "meta.json"))
+    assert "gfx950" in meta["arch"] and meta["cu_count"] > 0
