@@ -45,6 +45,51 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __
   }
 }
 
+// FP32 / TF32 output: the same sum and epilogue, stored as float (no rounding step)
+template <bool kVec>
+__global__ __launch_bounds__(kThreads) void splitk_reduce_f32_kernel(const float* __restrict__ partial,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ y, long long total, int split,
+                                                                     int M, int HWo, int relu) {
+  const long long quads = (total + 3) / 4;
+  for (long long qi = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; qi < quads;
+       qi += static_cast<long long>(gridDim.x) * kThreads) {
+    const long long i0 = qi * 4;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < split; ++z) {
+      if (kVec) {
+        s += *reinterpret_cast<const f32x4*>(partial + z * total + i0);
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (i0 + e < total) s[e] += partial[z * total + i0 + e];
+      }
+    }
+    for (int e = 0; e < 4; ++e) {
+      if (i0 + e >= total) break;
+      float v = s[e];
+      if (bias) v += bias[((i0 + e) / HWo) % M];
+      if (relu) v = fmaxf(v, 0.f);
+      if (kVec) s[e] = v;
+      else y[i0 + e] = v;
+    }
+    if (kVec) *reinterpret_cast<f32x4*>(y + i0) = s;
+  }
+}
+
+void launch_f32(const float* partial, const void* bias, void* y, long long total, int split, int M, int HWo, int relu,
+                hipStream_t s) {
+  long long blocks = ((total + 3) / 4 + kThreads - 1) / kThreads;
+  if (blocks > (1 << 20)) blocks = 1 << 20;
+  const bool vec = (total % 4) == 0 && (reinterpret_cast<uintptr_t>(partial) & 15u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+  if (vec)
+    hipLaunchKernelGGL((splitk_reduce_f32_kernel<true>), dim3(unsigned(blocks)), dim3(kThreads), 0, s, partial,
+                       static_cast<const float*>(bias), static_cast<float*>(y), total, split, M, HWo, relu);
+  else
+    hipLaunchKernelGGL((splitk_reduce_f32_kernel<false>), dim3(unsigned(blocks)), dim3(kThreads), 0, s, partial,
+                       static_cast<const float*>(bias), static_cast<float*>(y), total, split, M, HWo, relu);
+}
+
 template <typename E>
 void launch(const float* partial, const void* bias, void* y, long long total, int split, int M, int HWo, int relu,
             hipStream_t s) {
@@ -72,6 +117,8 @@ extern "C" int gie_hip_splitk_reduce(int dtype, const float* partial, const void
     launch<Fp16>(partial, bias, y, total, split, out_channels, hw_out, relu ? 1 : 0, s);
   else if (dtype == GIE_HIP_BF16)
     launch<Bf16>(partial, bias, y, total, split, out_channels, hw_out, relu ? 1 : 0, s);
+  else if (dtype == GIE_HIP_FP32 || dtype == GIE_HIP_TF32)
+    launch_f32(partial, bias, y, total, split, out_channels, hw_out, relu ? 1 : 0, s);
   else
     return GIE_HIP_EUNSUPPORTED;
   const hipError_t e = hipGetLastError();

@@ -11,6 +11,7 @@ void register_mfma_family(std::vector<KernelDesc>& out);  // mfma_family.cpp
 void register_halo_family(std::vector<KernelDesc>& out);  // halo_family.cpp
 void register_band_family(std::vector<KernelDesc>& out);  // band_family.cpp
 void register_pw_family(std::vector<KernelDesc>& out);    // pw_family.cpp
+void register_f32_family(std::vector<KernelDesc>& out);   // f32_family.cpp
 
 std::string KernelDesc::describe() const {
   std::ostringstream os;
@@ -29,6 +30,7 @@ std::vector<KernelDesc>& registry_storage() {
     register_halo_family(r);
     register_mfma_family(r);
     register_pw_family(r);  // after mfma: its unaligned-pointer fallback is an mfma entry
+    register_f32_family(r);
     std::set<std::string> names;
     for (const auto& k : r) {
       if (!names.insert(k.name).second) throw Error(StatusCode::kInternal, "duplicate kernel name " + k.name);

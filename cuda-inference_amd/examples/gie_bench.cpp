@@ -10,9 +10,10 @@
 //   * times steady-state launches with HIP events (time_stream_work) and derives TFLOP/s and images/s;
 //   * appends one JSON line to results.jsonl and one row to results.csv. Unsupported combinations, failed
 //     validations and errors are rows too, with a status and a reason: nothing is dropped.
-// Backends: tensor_core (the MFMA families), dispatcher, cpu_reference. The reference's other backend names
-// (direct, im2col_gemm, simt_tiled, implicit_gemm, cudnn, cudnn_gemm, cutlass) are accepted and produce
-// "unsupported" rows that say why. With only cpu_reference requested the harness runs without a GPU.
+// Backends: tensor_core (the FP16/BF16/TF32 MFMA families), implicit_gemm (the FP32 MFMA family), dispatcher,
+// cpu_reference. The reference's other backend names (direct, im2col_gemm, simt_tiled, cudnn, cudnn_gemm,
+// cutlass) are accepted and produce "unsupported" rows that say why. With only cpu_reference requested the
+// harness runs without a GPU.
 #include <hip/hip_runtime.h>
 #include <unistd.h>
 
@@ -54,7 +55,7 @@ namespace {
 struct Options {
   std::string workloads = "examples/workloads.json";
   std::string split_label;
-  std::vector<std::string> backends = {"tensor_core", "dispatcher"};
+  std::vector<std::string> backends = {"tensor_core", "implicit_gemm", "dispatcher"};
   std::vector<std::string> kernels;
   std::vector<Precision> precisions = {Precision::kFp32, Precision::kFp16};
   std::string mode = "tuned";
@@ -83,12 +84,12 @@ const char* kUsage =
     "  --workloads FILE        workload JSON {\"workloads\": [{\"name\", \"category\", B, C, H, W, O, K|Kh,Kw,\n"
     "                          S|Sh,Sw, P|Ph,Pw, bias, relu}], \"split\"} (default examples/workloads.json)\n"
     "  --split LABEL           split label recorded in every row (default: the file's \"split\")\n"
-    "  --backends LIST         tensor_core,dispatcher,cpu_reference (default tensor_core,dispatcher); the\n"
-    "                          reference's direct,im2col_gemm,simt_tiled,implicit_gemm,cudnn,cudnn_gemm,cutlass\n"
-    "                          give 'unsupported' rows\n"
+    "  --backends LIST         tensor_core,implicit_gemm,dispatcher,cpu_reference (default tensor_core,\n"
+    "                          implicit_gemm,dispatcher); the reference's direct,im2col_gemm,simt_tiled,cudnn,\n"
+    "                          cudnn_gemm,cutlass give 'unsupported' rows\n"
     "  --kernels LIST          also time these registered kernels by name (backend column 'kernel')\n"
     "  --precisions LIST       fp32,fp16,bf16,tf32 (default fp32,fp16)\n"
-    "  --mode tuned|fixed|both configuration policy of tensor_core\n"
+    "  --mode tuned|fixed|both configuration policy of tensor_core and implicit_gemm\n"
     "  --fusion fused|unfused|both   unfused = conv without epilogue + separate bias and ReLU passes\n"
     "  --warmup N --samples N --min-sample-ms X   timing protocol (defaults 5, 30, 1.0)\n"
     "  --flush-l2              evict L2 before every timed launch (cold-cache protocol)\n"
@@ -483,27 +484,37 @@ void measure(Bench& b, const ConvProblem& prob, Inputs& in, const KernelDesc& k,
   put_timing(r, t, prob);
 
   // multi-launch kernels: each stage alone, launched back to back on the workspace the full call filled
-  // (stages in launch order: 0 = weight/activation repack, 1 = convolution, 2 = split-K reduction)
+  // (0 = weight/activation repack where the family has one, 1 = convolution, 2 = split-K reduction)
   if (!unfused && k.launches > 1) {
-    const char* names[3] = {"stage_repack_us", "stage_conv_us", "stage_reduce_us"};
-    for (int st = 0; st < std::min(k.launches, 3); ++st)
-      r[names[st]] = time_stream_work([&](hipStream_t s) { run(s, st); }, b.stream, topt).median_us;
+    int split = 1;
+    for (const auto& kv : k.params)
+      if (kv.first == "split_k") split = kv.second;
+    const bool repack = k.launches - (split > 1 ? 1 : 0) >= 2;
+    auto stage_us = [&](int st) {
+      return time_stream_work([&](hipStream_t s) { run(s, st); }, b.stream, topt).median_us;
+    };
+    if (repack) r["stage_repack_us"] = stage_us(0);
+    r["stage_conv_us"] = stage_us(1);
+    if (split > 1) r["stage_reduce_us"] = stage_us(2);
     run(b.stream, -1);
     GIE_HIP_CHECK(hipStreamSynchronize(b.stream));
   }
   if (b.opt.e2e) r["host_sync_latency_us"] = host_sync_us(b, [&] { run(b.stream, -1); }, 10, 40);
 }
 
-// The reference's fixed configuration per backend, mapped to the MI355X registry.
+// The reference's fixed configuration per backend (benchmark_main.cpp:427-435), mapped to the MI355X registry.
 std::string fixed_kernel(const std::string& backend, Precision p) {
-  if (backend == "tensor_core") return std::string("mfma_") + to_string(p) + "_128x128x64_w4x2_s3_sk1";
+  if (backend == "tensor_core" && (p == Precision::kFp16 || p == Precision::kBf16))
+    return std::string("mfma_") + to_string(p) + "_128x128x64_w4x2_s3_sk1";
+  if (backend == "tensor_core" && p == Precision::kTf32) return "mfma_tf32_128x128x16_sk1";
+  if (backend == "implicit_gemm" && p == Precision::kFp32) return "implicit_gemm_fp32_128x128x16_mfma_sk1";
   return "";
 }
 
 bool reference_only_backend(const std::string& be, std::string* why) {
-  if (be == "direct" || be == "im2col_gemm" || be == "simt_tiled" || be == "implicit_gemm") {
+  if (be == "direct" || be == "im2col_gemm" || be == "simt_tiled") {
     *why = be + ": no such kernel family on gfx950; every registered kernel is an MFMA implicit GEMM "
-                "(backend tensor_core)";
+                "(backends tensor_core and implicit_gemm)";
     return true;
   }
   if (be == "cudnn" || be == "cudnn_gemm" || be == "cutlass") {
@@ -513,7 +524,10 @@ bool reference_only_backend(const std::string& be, std::string* why) {
   return false;
 }
 
-void run_tensor_core(Bench& b, const Workload& wl, const ConvProblem& prob, Inputs& in, const std::string& fusion) {
+// tensor_core / implicit_gemm rows: the backend's fixed configuration and/or its autotuned winner
+// (benchmark_main.cpp:437-482)
+void run_custom_backend(Bench& b, const Workload& wl, const ConvProblem& prob, Inputs& in, const std::string& backend,
+                        const std::string& fusion) {
   std::vector<std::string> modes;
   if (b.opt.mode == "both") modes = {"fixed", "tuned"};
   else modes = {b.opt.mode};
@@ -523,19 +537,18 @@ void run_tensor_core(Bench& b, const Workload& wl, const ConvProblem& prob, Inpu
     conv.activation = Activation::kNone;
   }
   for (const std::string& mode : modes) {
-    Value r = new_row(b, wl, prob, fusion, "tensor_core", mode);
+    Value r = new_row(b, wl, prob, fusion, backend, mode);
     try {
       const KernelDesc* k = nullptr;
       if (mode == "fixed") {
-        k = find_kernel(fixed_kernel("tensor_core", prob.precision));
+        k = find_kernel(fixed_kernel(backend, prob.precision));
         if (!k)
-          throw Error(StatusCode::kUnsupported, std::string("no fixed tensor_core kernel for ") +
-                                                    to_string(prob.precision));
+          throw Error(StatusCode::kUnsupported, "no fixed " + backend + " kernel for " + to_string(prob.precision));
         std::string why;
         if (!k->supports(conv, *b.dev, &why)) throw Error(StatusCode::kUnsupported, k->name + ": " + why);
       } else {
         TuneOptions to;
-        to.only_backend = Backend::kTensorCore;
+        to.only_backend = backend_from_string(backend);
         to.cache_path = b.opt.cache_path;
         to.force_retune = b.opt.retune;
         to.model_keep = b.opt.model_keep;
@@ -824,7 +837,8 @@ int main(int argc, char** argv) {
           for (const std::string& fusion : fusions) {
             if (fusion == "unfused" && !epilogue) continue;  // would repeat the fused rows
             for (const std::string& be : b.opt.backends) {
-              if (fusion == "unfused" && be != "tensor_core") continue;  // the fusion experiment is per kernel
+              // the fusion experiment is per kernel: the dispatcher and the CPU reference take no part in it
+              if (fusion == "unfused" && be != "tensor_core" && be != "implicit_gemm") continue;
               std::string why;
               if (reference_only_backend(be, &why)) {
                 Value r = new_row(b, wl, prob, fusion, be, "n/a");
@@ -834,7 +848,7 @@ int main(int argc, char** argv) {
               }
               if (be == "cpu_reference") run_cpu_reference(b, wl, prob, in, fusion);
               else if (be == "dispatcher") run_dispatcher(b, wl, prob, in, fusion);
-              else if (be == "tensor_core") run_tensor_core(b, wl, prob, in, fusion);
+              else if (be == "tensor_core" || be == "implicit_gemm") run_custom_backend(b, wl, prob, in, be, fusion);
               else {
                 Value r = new_row(b, wl, prob, fusion, be, "n/a");
                 mark_failed(r, "unsupported", "unknown backend " + be);

@@ -180,6 +180,10 @@ _HIP = {
     "gie_hip_conv_pw": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_splitk_reduce": ([_i, _vp, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _vp], _i),
     "gie_hip_bias_act": ([_i, _vp, _vp, ctypes.c_int64, _i, _i, _i, _vp], _i),
+    "gie_hip_f32_config_count": ([], _i),
+    "gie_hip_f32_config_tile_m": ([_i], _i),
+    "gie_hip_f32_check": ([_i, _GP, _vp], _i),
+    "gie_hip_conv_f32": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_reference_conv": ([_i, _GP, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_ceiling_mfma": ([_i, _i, _vp, _vp], _i),
     "gie_hip_ceiling_copy": ([_vp, _vp, _sz, _vp], _i),

@@ -22,6 +22,9 @@
  *   gie_hip_band_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
  *   gie_hip_conv_pw, gie_hip_pw_check both transposes + tcmma_kernel for 1x1 filters, fused (no repack)
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
+ *   gie_hip_conv_f32, _f32_check     implicit_gemm_kernel<<<>>> launch (FP32) and the TF32 path
+ *                                                                         src/kernels/implicit_gemm.cu:47-189,204-214
+ *   gie_hip_f32_config_*             the registered FP32 tile table        src/kernels/implicit_gemm.cu:218-268
  *   gie_hip_bias_act                 launch_bias_act / _bias_add / _relu   src/kernels/elementwise.cu:13-56
  *   gie_hip_reference_conv           gpu_conv2d_reference                  src/runtime/reference.cu:31-91
  *   gie_hip_ceiling_*                ceilings microbenchmarks              src/profiling/ceilings.cu:21-58
@@ -41,10 +44,12 @@ extern "C" {
 #define GIE_HIP_EINVAL (-1)      /* null pointer, bad size, shape the kernel's grid cannot cover */
 #define GIE_HIP_EUNSUPPORTED (-2) /* valid request this kernel configuration cannot run */
 
-/* element types; numbering follows gie::Precision (kFp32 = 0, kFp16 = 1, kBf16 = 2) */
+/* element types; numbering follows gie::Precision (kFp32 = 0, kFp16 = 1, kBf16 = 2, kTf32 = 3). TF32 is FP32
+   storage whose multiplier inputs are rounded to TF32 inside the kernel. */
 #define GIE_HIP_FP32 0
 #define GIE_HIP_FP16 1
 #define GIE_HIP_BF16 2
+#define GIE_HIP_TF32 3
 
 /* Convolution geometry as the kernels see it (dilation and groups are 1, enforced by the host). */
 typedef struct gie_conv_geom {
@@ -164,7 +169,21 @@ int gie_hip_pw_check(const gie_conv_geom* g, int* lds_bytes);
 int gie_hip_conv_pw(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
                     void* stream);
 
-/* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels])) */
+/* FP32 / TF32 convolution on MFMA 32x32x2 f32 (FP32 products and sums) straight from the caller's NCHW x and OIHW
+   w (float, 4-byte aligned; no workspace). TF32 rounds every multiplier input to TF32 (round to nearest, ties away
+   from zero) first. Configuration c computes tile_m(c) output channels x 128 pixels per workgroup.
+   split == 1: y = relu?(acc + bias), NCHW float. split > 1: partial[z][NCHW index] = sum over the z-th range of
+   the (tap, 16-channel chunk) stages [floor(T*z/split), floor(T*(z+1)/split)), T = kh*kw*ceil(C/16) (1 <= split
+   <= T); reduce with gie_hip_splitk_reduce (dtype GIE_HIP_FP32). */
+int gie_hip_f32_config_count(void);
+int gie_hip_f32_config_tile_m(int config);
+/* 0 when configuration `config` runs geometry g (offsets within 32 bits, grid limits), with T in *stages. */
+int gie_hip_f32_check(int config, const gie_conv_geom* g, int* stages);
+int gie_hip_conv_f32(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias,
+                     void* y, float* partial, int split, void* stream);
+
+/* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
+   dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */
 int gie_hip_splitk_reduce(int dtype, const float* partial, const void* bias, void* y, int64_t total, int split,
                           int out_channels, int hw_out, int relu, void* stream);
 

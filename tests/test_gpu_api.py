@@ -136,20 +136,29 @@ def test_invalid_problems_rejected_through_the_api():
 
 # ------------------------------------------------------------------------ test_dispatcher.cpp
 def test_capability_filter_reports_every_kernel_with_a_reason():
+    """tests/test_dispatcher.cpp:9-20: an FP32 problem has candidates, none of them a tensor-core kernel, and
+    every other registered kernel is rejected with a reason."""
     p = P(1, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, precision="fp32", bias=False, relu=False)
-    msg = expect_error("Unsupported", gie.select, p)
     names = gie.registry()
-    assert all(n in msg for n in names)  # every kernel accounted for, each with a reason
-    for n in names[:5]:
+    accepted, rejected = [], []
+    for n in names:
         ok, why = gie.kernel_supports(n, p)
-        assert not ok and why
+        (accepted if ok else rejected).append((n, why))
+    assert accepted and rejected and len(accepted) + len(rejected) == len(names)
+    assert all(gie.kernel_describe(n)["backend"] != "tensor_core" for n, _ in accepted)
+    assert all(why for _, why in rejected)
+    # forced to the tensor-core backend, the error lists every kernel of that backend with its reason
+    msg = expect_error("Unsupported", gie.select, p, backend="tensor_core")
+    tc = [n for n in names if gie.kernel_describe(n)["backend"] == "tensor_core"]
+    assert tc and all(f"- {n}: " in msg for n in tc)
 
 
 def test_precision_routes_to_matching_kernels():
-    for prec in ("fp16", "bf16"):
+    """tests/test_dispatcher.cpp:22-30, every precision of the reference included."""
+    for prec in ("fp32", "fp16", "bf16", "tf32"):
         p = P(2, 32, 28, 28, 64, 3, 3, 1, 1, 1, 1, precision=prec)
         ranked = gie.rank_by_model(p)
-        assert ranked
+        assert ranked, prec
         assert all(f"_{prec}_" in n for n, _ in ranked)
 
 

@@ -1,11 +1,12 @@
 """The gie_bench harness on the GPU: every row type of the reference's benchmarks/benchmark_main.cpp flow.
 
-Two small workloads (a 3x3 and a 1x1 layer) at fp16, bf16 and fp32 through tensor_core (fixed and tuned
-configurations), the dispatcher, a kernel named on the command line, the CPU reference and the copy rows, fused
-and unfused. Checks that each FP16/BF16 GPU row validated against the double reference before it was timed and
+Two small workloads (a 3x3 and a 1x1 layer) at fp16, bf16 and fp32 through tensor_core and implicit_gemm (fixed
+and tuned configurations), the dispatcher, a kernel named on the command line, the CPU reference and the copy
+rows, fused and unfused. Checks that each GPU row validated against the double reference before it was timed and
 carries positive timings, that the unfused rows (convolution + stand-alone bias and ReLU passes) validate under
-the two-rounding tolerance, that FP32 rows say 'unsupported' (no FP32 MFMA family is registered), and that the
-dispatcher row records its selection and the warm host overhead.
+the two-rounding tolerance, that a precision a backend has no kernel for gives an 'unsupported' row (tensor_core
+is FP16/BF16/TF32, implicit_gemm FP32), and that the dispatcher row records its selection and the warm host
+overhead.
 """
 import json
 import os
@@ -28,7 +29,7 @@ def test_gie_bench_rows_on_gpu(tmp_path):
     wl.write_text(json.dumps(doc))
     out = tmp_path / "res"
     named = "mfma_fp16_64x64x64_w2x2_s4_sk1"
-    cmd = [BIN, "--workloads", str(wl), "--backends", "tensor_core,dispatcher,cpu_reference,simt_tiled",
+    cmd = [BIN, "--workloads", str(wl), "--backends", "tensor_core,implicit_gemm,dispatcher,cpu_reference,simt_tiled",
            "--precisions", "fp16,bf16,fp32", "--mode", "both", "--fusion", "both", "--kernels", named,
            "--warmup", "1", "--samples", "3", "--min-sample-ms", "0.2", "--tune-samples", "2", "--model-keep", "3",
            "--cache", str(tmp_path / "tune.json"), "--e2e", "--out", str(out), "--tag", "gpu"]
@@ -73,8 +74,15 @@ def test_gie_bench_rows_on_gpu(tmp_path):
         for mode in ("fixed", "tuned"):
             (f,) = by[(w, "fp32", "tensor_core", "fused", mode)]
             assert f["status"] == "unsupported", f
+            for fusion in ("fused", "unfused"):
+                (g,) = by[(w, "fp32", "implicit_gemm", fusion, mode)]
+                assert g["status"] == "ok" and g["validated"] is True and g["tflops"] > 0, g
+                assert g["kernel"].startswith("implicit_gemm_fp32_"), g
+            for prec in ("fp16", "bf16"):
+                (u,) = by[(w, prec, "implicit_gemm", "fused", mode)]
+                assert u["status"] == "unsupported", u
         (fd,) = by[(w, "fp32", "dispatcher", "fused", "auto")]
-        assert fd["status"] == "unsupported", fd
+        assert fd["status"] == "ok" and fd["config"].startswith("selected implicit_gemm_fp32_"), fd
     # the 3x3 fixed configuration is a two-launch kernel (repack + convolution): both stages are timed
     (r,) = by[("l3x3", "fp16", "tensor_core", "fused", "fixed")]
     assert r["stage_repack_us"] > 0 and r["stage_conv_us"] > 0 and "stage_reduce_us" not in r
