@@ -227,6 +227,391 @@ __global__ __launch_bounds__(kPwNT, 2) void pw_kernel(const uint16_t* __restrict
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Weight-stationary streaming variant (C <= 256). The per-tile kernel above re-reads a 128 x 32 weight slice
+// and an X slice from L2 for every 128 x 128 output tile, and its 2 x 2 MFMA blocks per wave need ~256 B/clk of
+// LDS reads at the MFMA rate (more than the LDS delivers). Here one workgroup per CU (8 waves, two per SIMD) keeps
+// 256 filters x all C input channels in VGPRs for its whole life and streams one contiguous range of 64-pixel
+// blocks of the flattened B*H*W pixel axis through a four-stage LDS ring:
+//   * the weights come in once per workgroup: 256 filters x C by LDS-DMA into the LDS the ring and the output
+//     tiles use later, laid out [k-step][k-half][filter] in 16-byte units so every wave reads its B operands
+//     (filters 64*(w%4) .. +63, W[o][16j + 8*(lane/32) ..]) with conflict-free ds_read_b128;
+//   * block i = X[b][0 .. C)[p .. p+63] as two [channel][32 pixels] halves with 64-byte rows (16-byte chunks by
+//     LDS-DMA; a block may straddle two images, each 8-pixel chunk is addressed on its own, H*W % 8 == 0);
+//   * wave w takes pixel half w/4 against its 64 filters: A fragments by ds_read_b64_tr_b16 (rows k..k+3 of a
+//     16-lane group are 64 bytes apart, the two groups of a half-wave 32 bytes: no bank conflicts), 2 MFMA chains;
+//     the bias enters as one more k-step (A = 1 at k = 0, B = bias), after the real ones;
+//   * the epilogue of block i runs spread over the k-steps of block i+1 (two accumulator sets): ReLU + one
+//     rounding, the 64 x 32 tile into the wave's own 4 KiB LDS tile, then 16-byte stores of whole 64-byte rows.
+// Only X travels from L2 to LDS per block. The loads into the ring and the stores are issued through inline
+// assembly in a fixed order so the waits can count them (vmcnt counts both, in issue order). The workgroups that
+// share a pixel range (the 256-filter blocks of O) sit on one XCD (slot L -> XCD L % 8), so each X block comes
+// from HBM once.
+constexpr int kSwO = 256;   // filters per workgroup
+constexpr int kSwP = 64;    // pixels per block (two halves of 32)
+constexpr int kSwNST = 4;   // LDS ring stages
+constexpr int kSwNW = 8;    // waves
+constexpr int kSwNT = kSwNW * 64;
+constexpr int kSwTile = 4096;  // per-wave output tile (64 filters x 32 pixels x 2 B)
+
+struct PwsGeom {
+  int C, HW, O, N;     // N = B*H*W pixels
+  int n_ob;            // 256-filter blocks
+  int n_ranges;        // pixel ranges (workgroups per filter block)
+  int n_blk;           // 64-pixel blocks over N
+  int x_bytes, w_bytes, y_bytes;
+  unsigned hw_magic;   // n / HW = (umulhi(n, magic) + ((n - umulhi) >> 1)) >> (shift - 1)
+  int hw_shift;
+  int relu;
+};
+
+__device__ __forceinline__ unsigned div_hw(unsigned n, const PwsGeom& g) {
+  const unsigned t = __umulhi(n, g.hw_magic);
+  return (t + ((n - t) >> 1)) >> (g.hw_shift - 1);
+}
+
+// The hardware reads the data VGPRs of a store wider than 8 bytes after issue: a VALU write to them in the next
+// cycle (the compiler does not look inside inline assembly for this hazard) would change what is stored, so the
+// store carries its own wait state.
+__device__ __forceinline__ void store16(v4i rsrc, int voff, u32x4 v) {
+  asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1" ::"v"(v), "v"(voff), "s"(rsrc) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Register loads the compiler does not see as loads (so it inserts no waits of its own inside the streaming
+// loop): valid only after a counted wait_vm, followed by touch() so every use depends on that wait.
+__device__ __forceinline__ u32x4 load16_asm(v4i rsrc, int voff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc));
+  return v;
+}
+__device__ __forceinline__ uint32_t load2_asm(v4i rsrc, int voff) {
+  uint32_t v;
+  asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ void touch_v(T& v) {
+  asm volatile("" : "+v"(v));
+}
+// transposing 8-byte LDS read through a pointer, so constant offsets fold into the instruction's offset field
+typedef __attribute__((address_space(3))) const unsigned char lds_cu8;
+__device__ __forceinline__ u32x2 lds_tr8p(lds_cu8* p) {
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) v4s*>(const_cast<__attribute__((address_space(3))) unsigned char*>(p)));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// two FP32 values -> two 16-bit values in one register (gfx950 v_cvt_pk_{f16,bf16}_f32, round to nearest even)
+template <typename E>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<Fp16>(float a, float b) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), h2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<Bf16>(float a, float b) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), b2));
+}
+
+// packed ReLU on two rounded 16-bit values: max(round(v), 0) == round(max(v, 0)) (rounding is monotonic and
+// keeps the sign); v_pk_max_f16 for FP16, the FP32 max before rounding for BF16 (no packed BF16 max)
+template <typename E>
+__device__ __forceinline__ uint32_t relu2(uint32_t h) {
+  if constexpr (E::kDtype == GIE_HIP_FP16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(h2, h), (h2){0, 0}));
+  } else {
+    return h;
+  }
+}
+
+// v if ok, else the out-of-range offset, with bit operations (a conditional would become an exec-mask branch)
+__device__ __forceinline__ unsigned sel_or_out(bool ok, unsigned v) {
+  const unsigned m = 0u - unsigned(ok);
+  return (v & m) | (unsigned(kOut) & ~m);
+}
+
+// BIG: H*W >= 64, so a 64-pixel block spans at most two images and the per-lane pixel offsets follow from the
+// block's (image, pixel) pair, computed once per block in scalar registers; otherwise each lane divides.
+template <typename E, int KS, bool RELU, bool BIG>
+__global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                       const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                       PwsGeom g) {
+  constexpr int KL = KS / 4;              // 1 KiB ring units per wave per block (2*KS units over 8 waves)
+  constexpr int HB = KS * 1024;           // bytes per pixel half of a stage: 16*KS channels x 32 pixels x 2 B
+  constexpr int SB = 2 * HB;              // bytes per stage
+  constexpr int WL = KS * 8 * 1024 / (kSwNW * 1024);  // 1 KiB weight units per wave (256 x 16KS x 2 B in all)
+  constexpr int ST_W = 4;                 // stores per wave per block
+  constexpr int NST = kSwNST;
+  constexpr int W_OFF = SB;               // weights land on stages 1 .. NST-1 and the output tiles
+  constexpr bool kBf = E::kDtype == GIE_HIP_BF16;
+  static_assert(KS == 4 || KS == 8 || KS == 16, "16-channel k-steps");
+  static_assert((NST - 1) * SB + kSwNW * kSwTile >= KS * 8 * 1024, "the weights fit the space they are staged in");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fg = wave & 3, ph = wave >> 2;  // filter group (64 filters), pixel half of each block
+  static_assert(kSwP == 64, "BIG (one image wrap at most per block) assumes 64-pixel blocks and H*W >= 64");
+
+  // ---- workgroup -> (filter block, pixel range); the n_ob workgroups of one range share an XCD ----
+  const int L = int(blockIdx.x);
+  const int xcd = L & 7, rr = L >> 3;
+  const int ob = rr % g.n_ob, range = (rr / g.n_ob) * 8 + xcd;
+  if (range >= g.n_ranges) return;  // workgroup-uniform padding slot
+  const int blk0 = int((long long)g.n_blk * range / g.n_ranges);
+  const int nblk = int((long long)g.n_blk * (range + 1) / g.n_ranges) - blk0;
+
+  const v4i xr = make_vsharp(x, g.x_bytes);
+  const v4i yr = make_vsharp(y, g.y_bytes);
+  const v4i wr = make_vsharp(w, g.w_bytes);
+  const v4i br = make_vsharp(bias, bias != nullptr ? g.O * 2 : 0);
+  const unsigned lds0 = lds_addr(lds);
+  const unsigned hw = unsigned(g.HW);
+  const int o0 = kSwO * ob;
+
+  // ---- ring loads: unit u = wave + 8*kb of a stage holds pixel half u / KS, channels 16*(u % KS) .. +15;
+  //      lane: channel 16*(u % KS) + lane/4, pixel chunk lane%4 ----
+  unsigned cx_off[KL], dx[KL];  // channel row offset (x_bytes past C: out of range), first pixel in the block
+#pragma unroll
+  for (int kb = 0; kb < KL; ++kb) {
+    const int u = wave + kSwNW * kb;
+    const int c = 16 * (u % KS) + (lane >> 2);
+    cx_off[kb] = c < g.C ? unsigned(c) * hw * 2u : unsigned(g.x_bytes);
+    dx[kb] = 32u * unsigned(u / KS) + 8u * unsigned(lane & 3);
+  }
+  const unsigned x_wrap = unsigned(g.C - 1) * hw * 2u;  // pixel p + d >= HW: same channel of the next image
+  const unsigned y_wrap = unsigned(g.O - 1) * hw * 2u;
+  // first pixel of block i: image b0 and pixel p0 (uniform), pixels left in the tensor from there
+  struct Base {
+    unsigned b0, p0, rem;
+    bool whole;  // the block lies inside one image and the tensor: every lane's pixels valid, no image wrap
+  };
+  auto base_of = [&](int i) {
+    Base r;
+    const unsigned n0 = unsigned(blk0 + i) * kSwP;
+    r.b0 = div_hw(n0, g);
+    r.p0 = n0 - r.b0 * hw;
+    r.rem = i < nblk ? unsigned(g.N) - n0 : 0u;
+    r.whole = BIG && r.p0 + kSwP <= hw && r.rem >= kSwP;
+    return r;
+  };
+  // lane constants of the common (whole-block) case: ring-load offset past the block's first pixel, per unit
+  unsigned x_lane[KL];
+#pragma unroll
+  for (int kb = 0; kb < KL; ++kb) x_lane[kb] = dx[kb] * 2u + cx_off[kb];
+  auto issue_unit = [&](int i, int st, const Base& bb, int kb) {
+    if (bb.whole) {  // uniform: one add
+      dma16(xr, lds0 + st * SB + (wave + kSwNW * kb) * 1024, int((bb.b0 * unsigned(g.C) * hw + bb.p0) * 2u + x_lane[kb]));
+    } else {
+      unsigned off;
+      if constexpr (BIG) {
+        const unsigned xs0 = (bb.b0 * unsigned(g.C) * hw + bb.p0) * 2u;
+        off = sel_or_out(dx[kb] < bb.rem, xs0 + dx[kb] * 2u + (bb.p0 + dx[kb] >= hw ? x_wrap : 0u));
+      } else {
+        const unsigned n = unsigned(blk0 + i) * kSwP + dx[kb];
+        const unsigned b = div_hw(n, g), p = n - b * hw;
+        off = sel_or_out(i < nblk && n < unsigned(g.N), (b * unsigned(g.C) * hw + p) * 2u);
+      }
+      dma16(xr, lds0 + st * SB + (wave + kSwNW * kb) * 1024, int(off + cx_off[kb]));
+    }
+  };
+  auto issue = [&](int i, int st, const Base& bb) {
+#pragma unroll
+    for (int kb = 0; kb < KL; ++kb) issue_unit(i, st, bb, kb);
+  };
+
+  // ---- prologue 1: block 0 into stage 0, the weights into the rest of LDS, the lane's bias values ----
+  issue(0, 0, base_of(0));
+#pragma unroll
+  for (int t = 0; t < WL; ++t) {
+    // 16-byte unit e = 64*(wave + 8t) + lane of the weight area: filter e % 256, k-half (e / 256) % 2, k-step
+    // e / 512 (the layout the B-operand reads below want)
+    const int e = 64 * (wave + kSwNW * t) + lane;
+    const int o = o0 + (e & 255), k = 16 * (e >> 9) + 8 * ((e >> 8) & 1);
+    dma16(wr, lds0 + W_OFF + (wave + kSwNW * t) * 1024, (o < g.O && k < g.C) ? (o * g.C + k) * 2 : kOut);
+  }
+  uint32_t braw[2];
+  int o_lane[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    o_lane[nb] = o0 + 64 * fg + 32 * nb + (lane & 31);
+    braw[nb] = load2_asm(br, o_lane[nb] < g.O && lane < 32 ? o_lane[nb] * 2 : kOut);
+  }
+  wait_vm<0>();
+  touch_v(braw[0]);
+  touch_v(braw[1]);
+  __syncthreads();
+  u32x4 wf[2][KS];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      const unsigned e = unsigned(512 * j + 256 * (lane >> 5) + 64 * fg + 32 * nb + (lane & 31));
+      wf[nb][j] = lds_b128(lds0 + W_OFF + e * 16u);
+    }
+  stage_barrier();  // every wave holds its weights (lgkmcnt(0) in the barrier): the ring may overwrite them
+
+  // ---- prologue 2: blocks 1 .. NST-2 in flight ----
+#pragma unroll
+  for (int st = 1; st < NST - 1; ++st) issue(st, st, base_of(st));
+
+  // Ring load D(i+1) has landed for this wave once at most (loads issued after it) remain: the later ring loads
+  // (NST-2 blocks) and the store batches issued since. Block j's ring load goes out during the MFMAs of block
+  // j-NST+1; pixel half 0 stores block j after its MFMAs, pixel half 1 stores block j-1 before them, so at the end
+  // of block i that is min(i + 1, NST - 1) or min(i, NST - 2) store batches.
+  auto wait_next = [&](int i) {
+    static_assert(NST >= 3 && NST <= 6, "wait_next enumerates the warm-up blocks of a 3- to 6-stage ring");
+    const int k = ph == 0 ? (i + 1 < NST - 1 ? i + 1 : NST - 1) : (i < NST - 2 ? i : NST - 2);
+    if (k == 0) wait_vm<KL * (NST - 2)>();
+    else if (k == 1) wait_vm<KL * (NST - 2) + ST_W * 1>();
+    else if (k == 2) wait_vm<KL * (NST - 2) + ST_W * (2 < NST - 1 ? 2 : NST - 1)>();
+    else if (k == 3) wait_vm<KL * (NST - 2) + ST_W * (3 < NST - 1 ? 3 : NST - 1)>();
+    else if (k == 4) wait_vm<KL * (NST - 2) + ST_W * (4 < NST - 1 ? 4 : NST - 1)>();
+    else wait_vm<KL * (NST - 2) + ST_W * (NST - 1)>();
+  };
+  static_assert(KL * (NST - 2) + ST_W * (NST - 1) < 64, "vmcnt range");
+
+  // The bias enters as one more MFMA k-step after the real ones: A = 1 at k = 0 for every pixel, B = bias at
+  // k = 0 for the lane's filter (lanes 0-31 carry k = 0..7). The single non-zero product is exact, so the sum is
+  // acc + bias rounded once, the order of the reference's epilogue.
+  const uint32_t one = kBf ? 0x3F80u : 0x3C00u;
+  const u32x4 a_one = lane < 32 ? u32x4{one, 0u, 0u, 0u} : u32x4{0u, 0u, 0u, 0u};
+  const u32x4 b_bias[2] = {u32x4{braw[0] & 0xffffu, 0u, 0u, 0u}, u32x4{braw[1] & 0xffffu, 0u, 0u, 0u}};
+
+  // ---- epilogue of the previous block, spread over the k-steps of the current one ----
+  // The accumulators hold, per lane, filter o_lane[nb] and pixels 8q + 4*(lane/32) + 0..3 of the wave's half.
+  // They go through the wave's LDS tile [64 filters][32 pixels] (64-byte rows, the 8-byte granule g of row r at
+  // g ^ ((r/4) & 7), so the granule writes of 32 rows and the 16-byte row reads are free of bank conflicts) and
+  // leave as 16-byte stores of 16 whole 64-byte rows per instruction.
+  const unsigned stg = lds0 + unsigned(NST * SB) + unsigned(wave) * kSwTile;
+  typedef __attribute__((address_space(3))) u32x2 lds_u32x2_t;
+  typedef __attribute__((address_space(3))) const u32x4 lds_cu32x4_t;
+  // Tile layout: row r (64 bytes) holds filter 64fg + r; its 8-byte granule g sits at g ^ (2 * ((r / 4) & 3)).
+  // Granule writes (q, nb): row 32nb + lane%32, granule 2q + lane/32; the swizzle keeps granule pairs together, so
+  // a 16-byte segment s of row r is the 16-byte chunk s ^ ((r / 4) & 3) (2-way bank conflict on the writes, none
+  // on the reads).
+  lds_u32x2_t* w_q[4];
+  {
+    const unsigned f = (unsigned(lane) >> 2) & 3u, h = unsigned(lane) >> 5;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w_q[q] = reinterpret_cast<lds_u32x2_t*>(size_t(stg + unsigned(lane & 31) * 64u + (((unsigned(q) ^ f) << 1 | h) << 3)));
+  }
+  // row read t covers rows 16t + lane/4 ((r / 4) & 3 = (lane / 16) & 3 for every t), 16-byte segment lane%4
+  lds_cu32x4_t* const r_base = reinterpret_cast<lds_cu32x4_t*>(
+      size_t(stg + (unsigned(lane) >> 2) * 64u + (((unsigned(lane) & 3u) ^ ((unsigned(lane) >> 4) & 3u)) << 4)));
+  // y offset of the row of read t: filter o0 + 64fg + 16t + lane/4 (y_bytes past O: out of range)
+  unsigned o_row[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int o = o0 + 64 * fg + 16 * t + (lane >> 2);
+    o_row[t] = o < g.O ? unsigned(o) * hw * 2u : unsigned(g.y_bytes);
+  }
+  const unsigned d_y = 32u * unsigned(ph) + 8u * unsigned(lane & 3);  // the lane's first pixel of a row segment
+  unsigned st_x = 0;                                                   // y offset of that pixel
+  auto seg_offset = [&](int i, const Base& bb) {
+    if (bb.whole) {
+      st_x = (bb.b0 * unsigned(g.O) * hw + bb.p0) * 2u + d_y * 2u;
+    } else if constexpr (BIG) {
+      const unsigned ys0 = (bb.b0 * unsigned(g.O) * hw + bb.p0) * 2u;
+      st_x = sel_or_out(d_y < bb.rem, ys0 + d_y * 2u + (bb.p0 + d_y >= hw ? y_wrap : 0u));
+    } else {
+      const unsigned n = unsigned(blk0 + i) * kSwP + d_y;
+      const unsigned b = div_hw(n, g), p = n - b * hw;
+      st_x = sel_or_out(n < unsigned(g.N), (b * unsigned(g.O) * hw + p) * 2u);
+    }
+  };
+  auto put = [&](const f32x16 (&acc)[2], int q, int nb) {
+    uint32_t h[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float v0 = acc[nb][4 * q + 2 * e], v1 = acc[nb][4 * q + 2 * e + 1];
+      if (RELU && kBf) {
+        v0 = fmaxf(v0, 0.f);
+        v1 = fmaxf(v1, 0.f);
+      }
+      h[e] = pack2<E>(v0, v1);
+      if (RELU && !kBf) h[e] = relu2<E>(h[e]);
+    }
+    w_q[q][nb * 256] = u32x2{h[0], h[1]};  // + 2048 bytes for the second 32-filter block
+  };
+  auto epilogue = [&](const f32x16 (&acc)[2], int i) {
+    seg_offset(i, base_of(i));
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) put(acc, q, nb);
+    // A wave's LDS accesses complete in issue order, so the reads see the writes once the compiler keeps that order
+    // (the tile is written as 8-byte and read as 16-byte vectors, which type-based alias analysis would separate).
+    asm volatile("" ::: "memory");
+    u32x4 v[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = r_base[t * 64];  // + 1024 bytes per 16 rows
+#pragma unroll
+    for (int t = 0; t < 4; ++t) store16(yr, int(st_x + o_row[t]), v[t]);
+  };
+
+  // ---- A-fragment addresses: 16-lane group g16 reads pixels 16*(g16&1) .. +15 of channel rows k0 .. k0+3,
+  //      k0 = 16j + 8*(g16>>1) + 4h; lane s of the group: row k0 + s/4, pixels +4*(s%4) ----
+  unsigned a_lane;
+  {
+    const int s = lane & 15, g16 = lane >> 4;
+    a_lane = unsigned(ph * HB + (8 * (g16 >> 1) + (s >> 2)) * 64 + (16 * (g16 & 1) + 4 * (s & 3)) * 2);
+  }
+  lds_cu8* const a_base = reinterpret_cast<lds_cu8*>(size_t(lds0 + a_lane));
+  // The two waves that share a SIMD (w and w+4: same filters, other pixel half) work out of phase: half 0 runs
+  // the MFMAs of block i and then its epilogue, half 1 the epilogue of block i-1 and then the MFMAs of block i,
+  // so one wave's epilogue overlaps the other's MFMAs and each wave needs one accumulator set.
+  f32x16 acc[2];
+  auto compute = [&](int i) {
+    lds_cu8* ab = a_base + (i % NST) * SB;
+    const int i_ld = i + NST - 1, st_ld = (i + NST - 1) % NST;  // the ring load that goes out meanwhile
+    const Base b_ld = base_of(i_ld);
+    acc[0] = f32x16{};
+    acc[1] = f32x16{};
+    // A fragments two k-steps ahead of the MFMAs that use them (LDS latency exceeds two MFMA issues)
+    constexpr int PF = 2;
+    u32x4 af[PF + 1];
+    auto read_a = [&](int j) {
+      const u32x2 lo = lds_tr8p(ab + j * 1024), hi = lds_tr8p(ab + j * 1024 + 256);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    };
+#pragma unroll
+    for (int j = 0; j < PF; ++j) af[j] = read_a(j);
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      if (j + PF < KS) af[(j + PF) % (PF + 1)] = read_a(j + PF);
+      acc[0] = E::mfma32(af[j % (PF + 1)], wf[0][j], acc[0]);
+      acc[1] = E::mfma32(af[j % (PF + 1)], wf[1][j], acc[1]);
+      // ring-load units between the MFMAs (issued in a burst they would wait behind the stores in the memory
+      // pipeline before the MFMAs could start)
+      if constexpr (KS >= 2 * KL) {
+        if (j % 2 == 1 && j / 2 < KL) issue_unit(i_ld, st_ld, b_ld, j / 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads PF steps ahead (the scheduler would cluster them)
+    }
+    acc[0] = E::mfma32(a_one, b_bias[0], acc[0]);
+    acc[1] = E::mfma32(a_one, b_bias[1], acc[1]);
+  };
+
+  for (int i = 0; i < nblk; ++i) {
+    if (ph == 1 && i > 0) epilogue(acc, i - 1);
+    compute(i);
+    if (ph == 0) epilogue(acc, i);
+    wait_next(i);  // block i+1 has landed (this wave's part)
+    stage_barrier();
+  }
+  if (ph == 1) epilogue(acc, nblk - 1);
+  wait_vm<0>();  // ring loads past the range still target this workgroup's LDS
+}
+
 // geometry checks shared by the capability query and the launch
 int pw_prepare(const gie_conv_geom* gg, PwGeom* g) {
   if (!gg) return GIE_HIP_EINVAL;
@@ -258,6 +643,46 @@ int pw_prepare(const gie_conv_geom* gg, PwGeom* g) {
   return GIE_HIP_OK;
 }
 
+// geometry checks of the streaming variant, shared by its capability query and its launch
+int pws_prepare(const gie_conv_geom* gg, int cu_count, PwsGeom* g, int* ks) {
+  PwGeom base;
+  if (int rc = pw_prepare(gg, &base)) return rc;
+  if (gg->in_channels > 16 * 16) return GIE_HIP_EUNSUPPORTED;  // weights of 256 filters x C must fit the VGPRs
+  const long long n = static_cast<long long>(gg->batch) * gg->in_h * gg->in_w;
+  const long long yb = n * gg->out_channels * 2;
+  if (yb >= 0x7fffffffLL || n >= 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
+  g->C = gg->in_channels;
+  g->HW = base.HW;
+  g->O = gg->out_channels;
+  g->N = int(n);
+  g->n_ob = (g->O + kSwO - 1) / kSwO;
+  g->n_blk = int((n + kSwP - 1) / kSwP);
+  const int target = std::max(1, cu_count / g->n_ob);  // one workgroup per CU
+  g->n_ranges = std::max(1, std::min(g->n_blk, target));
+  const long long slots = static_cast<long long>((g->n_ranges + 7) / 8) * 8 * g->n_ob;
+  if (slots > 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
+  g->x_bytes = base.x_bytes;
+  g->w_bytes = base.w_bytes;
+  g->y_bytes = int(yb);
+  // n / HW for 32-bit n: l = ceil(log2 HW), magic = floor(2^32 (2^l - HW) / HW) + 1 (HW >= 8)
+  int l = 0;
+  while ((1LL << l) < g->HW) ++l;
+  g->hw_shift = l;
+  g->hw_magic = unsigned((((1ULL << l) - unsigned(g->HW)) << 32) / unsigned(g->HW) + 1);
+  g->relu = base.relu;
+  const int k16 = (g->C + 15) / 16;
+  *ks = k16 <= 4 ? 4 : k16 <= 8 ? 8 : 16;
+  return GIE_HIP_OK;
+}
+
+int device_cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
 }  // namespace
 }  // namespace gie_hip
 
@@ -285,6 +710,51 @@ extern "C" int gie_hip_conv_pw(int dtype, const gie_conv_geom* gg, const void* x
   const Fn fn = dtype == GIE_HIP_BF16 ? &pw_kernel<Bf16> : &pw_kernel<Fp16>;
   const long long slots = static_cast<long long>((g.n_tiles + 7) / 8) * 8 * g.n_ot;
   hipLaunchKernelGGL(fn, dim3(unsigned(slots)), dim3(kPwNT), kPwLds, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                     static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GIE_HIP_OK : int(e);
+}
+
+extern "C" int gie_hip_pws_check(const gie_conv_geom* g, int* lds_bytes) {
+  PwsGeom pg;
+  int ks = 0;
+  const int rc = pws_prepare(g, 256, &pg, &ks);
+  if (rc == GIE_HIP_OK && lds_bytes) *lds_bytes = kSwNST * 2 * ks * 1024 + kSwNW * kSwTile;
+  return rc;
+}
+
+extern "C" int gie_hip_conv_pws(int dtype, const gie_conv_geom* gg, const void* x, const void* w, const void* bias,
+                                void* y, void* stream) {
+  if (!gg || !x || !w || !y) return GIE_HIP_EINVAL;
+  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
+  if (bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) return GIE_HIP_EINVAL;
+  PwsGeom g;
+  int ks = 0;
+  if (int rc = pws_prepare(gg, device_cu_count(), &g, &ks)) return rc;
+  // 16-byte chunks into LDS, 16-byte weight loads, 8-byte stores
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
+      (reinterpret_cast<uintptr_t>(y) & 7u))
+    return GIE_HIP_EUNSUPPORTED;
+  using Fn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, PwsGeom);
+  static const Fn table[2][3][2][2] = {
+      {{{&pws_kernel<Fp16, 4, false, false>, &pws_kernel<Fp16, 4, false, true>},
+        {&pws_kernel<Fp16, 4, true, false>, &pws_kernel<Fp16, 4, true, true>}},
+       {{&pws_kernel<Fp16, 8, false, false>, &pws_kernel<Fp16, 8, false, true>},
+        {&pws_kernel<Fp16, 8, true, false>, &pws_kernel<Fp16, 8, true, true>}},
+       {{&pws_kernel<Fp16, 16, false, false>, &pws_kernel<Fp16, 16, false, true>},
+        {&pws_kernel<Fp16, 16, true, false>, &pws_kernel<Fp16, 16, true, true>}}},
+      {{{&pws_kernel<Bf16, 4, false, false>, &pws_kernel<Bf16, 4, false, true>},
+        {&pws_kernel<Bf16, 4, true, false>, &pws_kernel<Bf16, 4, true, true>}},
+       {{&pws_kernel<Bf16, 8, false, false>, &pws_kernel<Bf16, 8, false, true>},
+        {&pws_kernel<Bf16, 8, true, false>, &pws_kernel<Bf16, 8, true, true>}},
+       {{&pws_kernel<Bf16, 16, false, false>, &pws_kernel<Bf16, 16, false, true>},
+        {&pws_kernel<Bf16, 16, true, false>, &pws_kernel<Bf16, 16, true, true>}}}};
+  const Fn fn = table[dtype == GIE_HIP_BF16 ? 1 : 0][ks == 4 ? 0 : ks == 8 ? 1 : 2][g.relu ? 1 : 0][g.HW >= kSwP ? 1 : 0];
+  const int lds = kSwNST * 2 * ks * 1024 + kSwNW * kSwTile;  // ring + one 4 KiB output tile per wave
+  if (int rc = set_lds_limit(reinterpret_cast<const void*>(fn), lds)) return rc;
+  const long long slots = static_cast<long long>((g.n_ranges + 7) / 8) * 8 * g.n_ob;
+  hipLaunchKernelGGL(fn, dim3(unsigned(slots)), dim3(kSwNT), lds, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
                      static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), g);
   const hipError_t e = hipGetLastError();

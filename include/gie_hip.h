@@ -22,6 +22,7 @@
  *   gie_hip_band_config_*, _check    the registered tile table / supports  src/kernels/tensor_core_mma.cu:280-295,370-388
  *   gie_hip_conv_pw, gie_hip_pw_check both transposes + tcmma_kernel for 1x1 filters, fused (no repack)
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
+ *   gie_hip_conv_pws, _pws_check     the same, weight-stationary streaming form for in_channels <= 256
  *   gie_hip_conv_f32, _f32_check     implicit_gemm_kernel<<<>>> launch (FP32) and the TF32 path
  *                                                                         src/kernels/implicit_gemm.cu:47-189,204-214
  *   gie_hip_f32_config_*             the registered FP32 tile table        src/kernels/implicit_gemm.cu:218-268
@@ -181,6 +182,14 @@ int gie_hip_f32_config_tile_m(int config);
 int gie_hip_f32_check(int config, const gie_conv_geom* g, int* stages);
 int gie_hip_conv_f32(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias,
                      void* y, float* partial, int split, void* stream);
+
+/* Weight-stationary streaming form of gie_hip_conv_pw for in_channels <= 256 (same operands and result; x and w
+   16-byte aligned, y 8-byte aligned, GIE_HIP_EUNSUPPORTED otherwise): each workgroup holds 256 filters x C in
+   registers and streams a contiguous range of 32-pixel blocks of the flattened batch*h*w axis. One launch, no
+   workspace. *_check: 0 when the geometry qualifies, LDS bytes per workgroup in *lds_bytes. */
+int gie_hip_pws_check(const gie_conv_geom* g, int* lds_bytes);
+int gie_hip_conv_pws(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
+                     void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
    dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */
