@@ -1,0 +1,353 @@
+// Stem convolution (7x7 filter, stride 2, padding 3, in_channels <= 4) straight from NCHW on gfx950 matrix cores
+// (v_mfma_f32_32x32x16_{f16,bf16}, FP32 accumulation): no repack, no padded channels, one launch.
+//
+// The generic implicit GEMM pads C to 8 channels per tap (K = 49 * 8 = 392 for C = 3); the stem's reduction is
+// only C * 49 = 147 long and the layer is bound by writing Y (64 filters per pixel), so this kernel keeps the
+// reduction short and spends its effort on the stores.
+//   * K order: one group of 8 per (channel c, filter row kh): the even filter columns kw = 0, 2, 4, 6, then the
+//     odd ones kw = 1, 3, 5, then a zero. With stride 2 the 7 input pixels of one (c, kh) group are the input
+//     columns 2*ow - 3 .. 2*ow + 3, inside the 4 dwords of the row that start at column 2*ow - 4; reordered that
+//     way, the group's 16-byte operand is formed from those 4 dwords with 4 bit operations. 7*C groups plus one
+//     bias group (weights = bias, pixels = 1.0 at its first k), in k-steps of two groups: K = 176 for C = 3
+//     (147 useful).
+//   * A workgroup (one per CU, persistent) owns 64 filters and walks tiles of 2 output rows of one image (2 * out_w
+//     pixels, contiguous in each output plane). The tile's 2*2+5 input rows per channel sit in LDS with 4 zero
+//     dwords on each side (the horizontal padding); rows above or below the image are loaded as zeros. Wave 7
+//     streams rows: tile i+2's rows go straight into the third of three row buffers (buffer_load ... lds) while
+//     waves 0..6 multiply tile i. Waves 0..6 hold the 64 filters' operands in registers (2 x 32 columns x K);
+//     per 32-pixel block: two ds_read2_b32 and 4 bit operations per k-step, two MFMA chains. One barrier per tile.
+//   * MFMA roles: rows = pixels, columns = filters, so each lane's accumulators hold 4-pixel runs of one filter.
+//     Epilogue: ReLU, RNE rounding (the order of the reference's apply_epilogue,
+//     src/kernels/fused_epilogue.cuh:11-16), one v_permlane32_swap per register pair so each lane holds two
+//     8-pixel runs, and 16-byte stores (one run of one filter per lane; 16-byte stores reach ~5.7 TB/s on this
+//     output where 8-byte stores of 64-byte runs stay near 3.5 TB/s).
+//   * Grid: one 8-wave workgroup per CU; tiles are split into 8 contiguous ranges, one per XCD (blockIdx mod 8),
+//     so the input rows shared by neighbouring tiles are read into one L2.
+#include <algorithm>
+
+#include "lds_pipe.h"
+
+namespace gie_hip {
+namespace {
+
+constexpr int kStNT = 512;             // threads per workgroup: waves 0..6 multiply, wave 7 streams rows
+constexpr int kStCW = 7;               // multiplying waves
+constexpr int kStLoader = 7;           // the row-streaming wave
+constexpr int kStR = 2;                // output rows per tile
+constexpr int kStWR = 2 * kStR + 5;    // input rows per tile and channel
+constexpr int kStBufs = 3;             // row buffers: tile i read, i+1 landed, i+2 in flight
+constexpr int kStPad = 4;              // zero dwords left of each row (and at least 2 to its right)
+constexpr int kStLdsMax = 160 * 1024;
+
+struct StemGeom {
+  int N, C, H, W, O, OH, OW;
+  int n_rt;       // tiles per image
+  int n_tiles;    // tiles per filter group
+  int NB;         // 32-pixel blocks per tile
+  int G;          // workgroups per filter group (a multiple of 8)
+  int per_xcd;    // tiles per XCD range
+  int CPR;        // 16-byte chunks per input row (in_w / 8 <= 64)
+  int RS;         // LDS row stride in dwords: in_w / 2 + 8
+  int buf_bytes;  // one row buffer: C * WR * RS * 4
+  int rows_off;   // LDS byte offset of the row buffers (after the prologue's weights)
+  int x_bytes, y_bytes;
+};
+
+template <typename E>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<Fp16>(float a, float b) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), h2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<Bf16>(float a, float b) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), b2));
+}
+
+template <typename E>
+constexpr uint32_t one_bits() {
+  return E::kDtype == GIE_HIP_FP16 ? 0x3C00u : 0x3F80u;
+}
+
+template <typename E, int C, bool RELU>
+__global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                    StemGeom g) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NG = 7 * C;             // (channel, filter row) groups
+  constexpr int KS = (NG + 2) / 2;      // k-steps: NG groups + the bias group, two groups per step
+  constexpr int FW = C * 49;            // weights per filter
+  constexpr int NROW = C * kStWR;       // input rows per tile
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hi = lane >> 5, col = lane & 31;
+  const int og = blockIdx.x / g.G, L = blockIdx.x - og * g.G;
+  const int f0 = og * 64;
+  const int nf = min(64, g.O - f0);
+  auto rows = [&](int i) { return smem + g.rows_off + (i % kStBufs) * g.buf_bytes; };
+
+  // ---- tiles of this workgroup: XCD range, then every (G/8)-th tile of it
+  const int xcd = L & 7, step = g.G >> 3;
+  const int t0 = xcd * g.per_xcd + (L >> 3);
+  const int t_end = min(g.n_tiles, (xcd + 1) * g.per_xcd);
+  const int n_my = t0 < t_end ? (t_end - t0 + step - 1) / step : 0;
+  const int row_bytes = g.W * 2;
+  const size_t y_plane = size_t(g.OH) * g.OW;
+  const v4i xr = make_vsharp(x, g.x_bytes);
+  const v4i yr = make_vsharp(y, g.y_bytes);
+
+  // the rows of tile i into row buffer i % 3 (streaming wave): one load per row, lanes < in_w / 8 active (an
+  // inactive lane writes nothing), rows above or below the image read as zeros
+  auto load_rows = [&](int i) {
+    const int t = t0 + i * step;
+    const int n = t / g.n_rt, oh0 = (t - n * g.n_rt) * kStR;
+    unsigned char* dst = rows(i) + kStPad * 4;
+    if (lane < g.CPR) {
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int lr = 0; lr < kStWR; ++lr) {
+          const int ih = 2 * oh0 - 3 + lr;
+          const int voff = ih >= 0 && ih < g.H ? ((n * C + c) * g.H + ih) * row_bytes + lane * 16 : kOut;
+          dma16(xr, lds_addr(dst + (c * kStWR + lr) * g.RS * 4), voff);
+        }
+    }
+  };
+  if (wave == kStLoader) {
+    if (n_my > 0) load_rows(0);
+    if (n_my > 1) load_rows(1);
+  }
+  // the horizontal padding of every row buffer: zero once, never written again
+  for (int idx = tid; idx < kStBufs * NROW * 8; idx += kStNT) {
+    const int rw = idx >> 3, d = idx & 7;
+    const int dw = d < kStPad ? d : kStPad + g.W / 2 + (d - kStPad);
+    reinterpret_cast<uint32_t*>(smem + g.rows_off)[rw * g.RS + dw] = 0u;
+  }
+
+  // ---- the workgroup's 64 filters: raw OIHW block (16-byte aligned: 64 * C * 49 halves per group) and the bias
+  // into LDS, then the MFMA operands
+  uint16_t* wl = reinterpret_cast<uint16_t*>(smem);
+  constexpr int kWBytes = (64 * FW * 2 + 15) / 16 * 16;
+  constexpr int kFragBytes = 64 * KS * 2 * 16;
+  u32x4* frag = reinterpret_cast<u32x4*>(smem + kWBytes);
+  uint16_t* bl = reinterpret_cast<uint16_t*>(smem + kWBytes + kFragBytes);
+  {
+    constexpr int kW16 = (64 * FW * 2 / 16 + kStNT - 1) / kStNT;  // 16-byte chunks per thread
+    const int nh = nf * FW, n16 = nh >> 3;
+    const u32x4* w16 = reinterpret_cast<const u32x4*>(w + size_t(f0) * FW);
+    u32x4 tmp[kW16];
+#pragma unroll
+    for (int k = 0; k < kW16; ++k)
+      if (tid + k * kStNT < n16) tmp[k] = w16[tid + k * kStNT];
+    if (tid < nh - n16 * 8) wl[n16 * 8 + tid] = w[size_t(f0) * FW + n16 * 8 + tid];
+    if (tid < nf) bl[tid] = bias != nullptr ? bias[f0 + tid] : uint16_t(0);
+#pragma unroll
+    for (int k = 0; k < kW16; ++k)
+      if (tid + k * kStNT < n16) *reinterpret_cast<u32x4*>(wl + (tid + k * kStNT) * 8) = tmp[k];
+  }
+  __syncthreads();
+  // operand (filter f, k-step s, half h) = 8 halves of group 2s + h: kw 0, 2, 4, 6, 1, 3, 5, 0; the bias group
+  // holds (bias, 0, ...); groups past it are zero. Stored [f][s][h] x 16 bytes.
+  for (int idx = tid; idx < 64 * KS * 2; idx += kStNT) {
+    const int f = idx / (2 * KS), grp = idx - f * 2 * KS;  // grp = 2s + h
+    uint32_t h[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (f < nf) {
+      if (grp < NG) {
+        const uint16_t* p = wl + f * FW + (grp / 7) * 49 + (grp % 7) * 7;
+        h[0] = p[0], h[1] = p[2], h[2] = p[4], h[3] = p[6], h[4] = p[1], h[5] = p[3], h[6] = p[5];
+      } else if (grp == NG) {
+        h[0] = bl[f];
+      }
+    }
+    frag[idx] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+  }
+  __syncthreads();
+
+  if (wave == kStLoader) {
+    // ---- streaming wave: before the barrier that ends tile i, tile i+1's rows must have landed; tile i+2's are
+    // issued first and may stay in flight (this wave issues no other vector-memory operation in the loop)
+    wait_vm<0>();  // tile 0's rows (the weight loads above were waited for, and issued after them)
+    stage_barrier();
+    for (int i = 0; i < n_my; ++i) {
+      if (i + 2 < n_my) {
+        load_rows(i + 2);
+        wait_vm<NROW>();  // the NROW loads just issued may stay in flight
+      } else {
+        wait_vm<0>();
+      }
+      stage_barrier();
+    }
+    return;
+  }
+
+  u32x4 wa[2][KS];
+#pragma unroll
+  for (int fh = 0; fh < 2; ++fh)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) wa[fh][s] = frag[((fh * 32 + col) * KS + s) * 2 + hi];
+  // per-lane byte offset of the row each k-step reads, from the lane's (output row 0, column 0) position (the bias
+  // and zero groups read group 0: any valid address, replaced below)
+  int offs[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int grp = 2 * s + hi < NG ? 2 * s + hi : 0;
+    offs[s] = ((grp / 7) * kStWR + grp % 7) * g.RS * 4;
+  }
+  stage_barrier();  // tile 0's rows are in
+
+  // ---- multiplying waves: 32-pixel blocks wave, wave + 7, ... of tile i from row buffer i % 3
+  const int npix = kStR * g.OW;
+  for (int i = 0; i < n_my; ++i) {
+    const int t = t0 + i * step;
+    const int n = t / g.n_rt, oh0 = (t - n * g.n_rt) * kStR;
+    const unsigned char* rb = rows(i);
+    for (int blk = wave; blk < g.NB; blk += kStCW) {
+      const int p = blk * 32 + col;
+      const int pc = p < npix ? p : 0;
+      const int r = pc / g.OW, ow = pc - r * g.OW;
+      // row dwords ow-2 .. ow+1 (input columns 2*ow-4 .. 2*ow+3) sit at padded dwords ow+2 .. ow+5
+      const unsigned char* bp = rb + (2 * r * g.RS + ow + 2) * 4;
+      uint32_t d[KS][4];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(bp + offs[s]);
+        d[s][0] = q[0], d[s][1] = q[1], d[s][2] = q[2], d[s][3] = q[3];
+      }
+      f32x16 acc0 = {0}, acc1 = {0};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        // halves h0..h7 = input columns 2*ow-4 .. 2*ow+3; the group is (h1, h3, h5, h7, h2, h4, h6, 0)
+        u32x4 b;
+        b.x = (d[s][0] >> 16) | (d[s][1] & 0xffff0000u);  // kw 0, 2
+        b.y = (d[s][2] >> 16) | (d[s][3] & 0xffff0000u);  // kw 4, 6
+        b.z = (d[s][1] & 0xffffu) | (d[s][2] << 16);      // kw 1, 3
+        b.w = d[s][3] & 0xffffu;                          // kw 5, 0
+        const int grp = 2 * s + hi;
+        if (2 * s + 1 >= NG) {  // this step holds the bias group (and possibly the zero group)
+          if (grp == NG) b = u32x4{one_bits<E>(), 0u, 0u, 0u};
+          else if (grp > NG) b = u32x4{0u, 0u, 0u, 0u};
+        }
+        acc0 = E::mfma32(b, wa[0][s], acc0);  // rows: pixels; columns: filters
+        acc1 = E::mfma32(b, wa[1][s], acc1);
+      }
+      // epilogue: lane (hi, col) holds filter col of the half and pixels 8a + 4hi + (0..3), a = 0..3; one
+      // v_permlane32_swap per register pair trades the lower half's a = 2, 3 for the upper half's a = 0, 1, so the
+      // lower half holds pixels 0..15 and the upper half 16..31: two 16-byte stores per lane
+#pragma unroll
+      for (int fh = 0; fh < 2; ++fh) {
+        const f32x16& acc = fh ? acc1 : acc0;
+        uint32_t P[4][2];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            float v0 = acc[4 * a + 2 * j], v1 = acc[4 * a + 2 * j + 1];
+            if (RELU) v0 = fmaxf(v0, 0.0f), v1 = fmaxf(v1, 0.0f);
+            P[a][j] = pack2<E>(v0, v1);
+          }
+        const int f = f0 + fh * 32 + col;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          // lanes 32..63 of P[b] <-> lanes 0..31 of P[b + 2]
+          const auto s0 = __builtin_amdgcn_permlane32_swap(P[b][0], P[b + 2][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(P[b][1], P[b + 2][1], false, false);
+          const int p0 = blk * 32 + 16 * hi + 8 * b;  // 8 pixels of one output row (out_w % 8 == 0)
+          const bool ok = p0 < npix && oh0 + p0 / g.OW < g.OH && f < g.O;
+          const int voff = ok ? int(((size_t(n) * g.O + f) * y_plane + size_t(oh0) * g.OW + p0) * 2) : kOut;
+          store16(yr, voff, u32x4{s0[0], s1[0], s0[1], s1[1]});
+        }
+      }
+    }
+    stage_barrier();  // tile i's rows are no longer read; tile i+1's have landed
+  }
+}
+
+// Geometry of a stem launch; GIE_HIP_EUNSUPPORTED when the problem is not one this kernel runs.
+int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
+  if (!gg) return GIE_HIP_EINVAL;
+  if (gg->kernel_h != 7 || gg->kernel_w != 7 || gg->stride_h != 2 || gg->stride_w != 2 || gg->pad_h != 3 ||
+      gg->pad_w != 3)
+    return GIE_HIP_EUNSUPPORTED;
+  if (gg->in_channels < 1 || gg->in_channels > 4 || gg->batch < 1 || gg->out_channels < 1 || gg->in_h < 1 ||
+      gg->in_w < 16 || gg->in_w % 16 != 0 || gg->in_w > 512)
+    return GIE_HIP_EUNSUPPORTED;
+  if (gg->out_h != (gg->in_h - 1) / 2 + 1 || gg->out_w != gg->in_w / 2) return GIE_HIP_EINVAL;
+  const long long nx = 1LL * gg->batch * gg->in_channels * gg->in_h * gg->in_w;
+  const long long ny = 1LL * gg->batch * gg->out_channels * gg->out_h * gg->out_w;
+  if (2 * nx >= (1LL << 31) || 2 * ny >= (1LL << 31)) return GIE_HIP_EUNSUPPORTED;  // 32-bit byte offsets
+  g->N = gg->batch, g->C = gg->in_channels, g->H = gg->in_h, g->W = gg->in_w, g->O = gg->out_channels;
+  g->OH = gg->out_h, g->OW = gg->out_w;
+  g->CPR = g->W / 8;
+  g->RS = g->W / 2 + 2 * kStPad;
+  g->n_rt = (g->OH + kStR - 1) / kStR;
+  g->n_tiles = g->N * g->n_rt;
+  g->NB = (kStR * g->OW + 31) / 32;
+  g->G = std::max(8, std::min((g->n_tiles + 7) / 8 * 8, cus / 8 * 8));
+  g->per_xcd = (g->n_tiles + 7) / 8;
+  g->buf_bytes = g->C * kStWR * g->RS * 4;
+  const int ks = (7 * g->C + 2) / 2;
+  g->rows_off = (64 * g->C * 49 * 2 + 15) / 16 * 16 + 64 * ks * 2 * 16 + 128;  // weights, operands, bias
+  g->x_bytes = int(2 * nx);
+  g->y_bytes = int(2 * ny);
+  const long long grid = 1LL * g->G * ((g->O + 63) / 64);
+  if (grid >= (1LL << 31)) return GIE_HIP_EUNSUPPORTED;
+  const int total = g->rows_off + kStBufs * g->buf_bytes;
+  if (total > kStLdsMax) return GIE_HIP_EUNSUPPORTED;
+  if (lds) *lds = total;
+  return GIE_HIP_OK;
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+using StemFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, StemGeom);
+
+template <typename E, bool RELU>
+StemFn stem_fn(int c) {
+  switch (c) {
+    case 1: return &stem_kernel<E, 1, RELU>;
+    case 2: return &stem_kernel<E, 2, RELU>;
+    case 3: return &stem_kernel<E, 3, RELU>;
+    default: return &stem_kernel<E, 4, RELU>;
+  }
+}
+
+}  // namespace
+}  // namespace gie_hip
+
+using namespace gie_hip;
+
+extern "C" int gie_hip_stem_check(const gie_conv_geom* g, int* lds_bytes) {
+  StemGeom sg;
+  return stem_prepare(g, 256, &sg, lds_bytes);
+}
+
+extern "C" int gie_hip_conv_stem(int dtype, const gie_conv_geom* gg, const void* x, const void* w, const void* bias,
+                                 void* y, void* stream) {
+  if (!gg || !x || !w || !y) return GIE_HIP_EINVAL;
+  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
+  if (bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) return GIE_HIP_EINVAL;
+  StemGeom g;
+  int lds = 0;
+  if (int rc = stem_prepare(gg, device_cus(), &g, &lds)) return rc;
+  // 16-byte input row and weight loads, 16-byte output stores
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
+      (reinterpret_cast<uintptr_t>(y) & 15u))
+    return GIE_HIP_EUNSUPPORTED;
+  const bool bf = dtype == GIE_HIP_BF16;
+  const StemFn fn = bf ? (gg->relu ? stem_fn<Bf16, true>(g.C) : stem_fn<Bf16, false>(g.C))
+                       : (gg->relu ? stem_fn<Fp16, true>(g.C) : stem_fn<Fp16, false>(g.C));
+  if (int rc = set_lds_limit(reinterpret_cast<const void*>(fn), lds)) return rc;
+  const unsigned grid = unsigned(g.G * ((g.O + 63) / 64));
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kStNT), lds, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                     static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GIE_HIP_OK : int(e);
+}

@@ -51,6 +51,35 @@ __device__ __forceinline__ void dma16(v4i rsrc, unsigned lds_base, int voff) {
                : "m0");
 }
 
+// The hardware reads the data VGPRs of a store wider than 8 bytes after issue: a VALU write to them in the next
+// cycle (the compiler does not look inside inline assembly for this hazard) would change what is stored, so the
+// store carries its own wait state.
+__device__ __forceinline__ void store16(v4i rsrc, int voff, u32x4 v) {
+  asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1" ::"v"(v), "v"(voff), "s"(rsrc) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Register loads the compiler does not see as loads (so it inserts no waits of its own inside the streaming
+// loop): valid only after a counted wait_vm, followed by touch() so every use depends on that wait.
+__device__ __forceinline__ u32x4 load16_asm(v4i rsrc, int voff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc));
+  return v;
+}
+__device__ __forceinline__ uint32_t load2_asm(v4i rsrc, int voff) {
+  uint32_t v;
+  asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ void touch_v(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
 // Workgroup barrier for the load pipeline. __syncthreads() also emits a release fence, which the compiler
 // lowers to s_waitcnt vmcnt(0): that would wait for every prefetch in flight. Here the caller has already waited
 // for exactly the loads that must have landed (wait_vmcnt); this barrier only drains this wave's LDS accesses and

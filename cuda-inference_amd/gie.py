@@ -182,6 +182,8 @@ _HIP = {
     "gie_hip_bias_act": ([_i, _vp, _vp, ctypes.c_int64, _i, _i, _i, _vp], _i),
     "gie_hip_pws_check": ([_GP, _vp], _i),
     "gie_hip_conv_pws": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
+    "gie_hip_stem_check": ([_GP, _vp], _i),
+    "gie_hip_conv_stem": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_f32_config_count": ([], _i),
     "gie_hip_f32_config_tile_m": ([_i], _i),
     "gie_hip_f32_check": ([_i, _GP, _vp], _i),

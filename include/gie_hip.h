@@ -23,6 +23,8 @@
  *   gie_hip_conv_pw, gie_hip_pw_check both transposes + tcmma_kernel for 1x1 filters, fused (no repack)
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
  *   gie_hip_conv_pws, _pws_check     the same, weight-stationary streaming form for in_channels <= 256
+ *   gie_hip_conv_stem, _stem_check   transposes + tcmma_kernel for the 7x7 stride-2 stem (in_channels <= 4), fused
+ *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
  *   gie_hip_conv_f32, _f32_check     implicit_gemm_kernel<<<>>> launch (FP32) and the TF32 path
  *                                                                         src/kernels/implicit_gemm.cu:47-189,204-214
  *   gie_hip_f32_config_*             the registered FP32 tile table        src/kernels/implicit_gemm.cu:218-268
@@ -190,6 +192,14 @@ int gie_hip_conv_f32(int config, int dtype, const gie_conv_geom* g, const void* 
 int gie_hip_pws_check(const gie_conv_geom* g, int* lds_bytes);
 int gie_hip_conv_pws(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
                      void* stream);
+
+/* Stem convolution straight from NCHW x / OIHW w: 7x7 filter, stride 2, padding 3, 1 <= in_channels <= 4,
+   in_w % 16 == 0, fused bias + ReLU, dtype GIE_HIP_FP16 / _BF16 (x, w and y 16-byte aligned, bias 2-byte
+   aligned; GIE_HIP_EUNSUPPORTED for other alignments or geometries). One launch, no workspace.
+   *_check: 0 when the geometry qualifies, LDS bytes per workgroup in *lds_bytes. */
+int gie_hip_stem_check(const gie_conv_geom* g, int* lds_bytes);
+int gie_hip_conv_stem(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
+                      void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
    dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */
