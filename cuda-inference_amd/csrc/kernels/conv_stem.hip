@@ -10,8 +10,8 @@
 //     way, the group's 16-byte operand is formed from those 4 dwords with 4 bit operations. 7*C groups plus one
 //     bias group (weights = bias, pixels = 1.0 at its first k), in k-steps of two groups: K = 176 for C = 3
 //     (147 useful).
-//   * A workgroup (one per CU, persistent) owns 64 filters and walks tiles of 2 output rows of one image (2 * out_w
-//     pixels, contiguous in each output plane). The tile's 2*2+5 input rows per channel sit in LDS with 4 zero
+//   * A workgroup (one per CU, persistent) owns 64 filters and walks tiles of R = 4 (2 for wide rows) output rows of
+//     one image (R * out_w pixels, contiguous in each output plane). The tile's 2R+5 input rows per channel sit in LDS with 4 zero
 //     dwords on each side (the horizontal padding); rows above or below the image are loaded as zeros. Wave 7
 //     streams rows: tile i+2's rows go straight into the third of three row buffers (buffer_load ... lds) while
 //     waves 0..6 multiply tile i. Waves 0..6 hold the 64 filters' operands in registers (2 x 32 columns x K);
@@ -33,14 +33,13 @@ namespace {
 constexpr int kStNT = 512;             // threads per workgroup: waves 0..6 multiply, wave 7 streams rows
 constexpr int kStCW = 7;               // multiplying waves
 constexpr int kStLoader = 7;           // the row-streaming wave
-constexpr int kStR = 2;                // output rows per tile
-constexpr int kStWR = 2 * kStR + 5;    // input rows per tile and channel
 constexpr int kStBufs = 3;             // row buffers: tile i read, i+1 landed, i+2 in flight
 constexpr int kStPad = 4;              // zero dwords left of each row (and at least 2 to its right)
 constexpr int kStLdsMax = 160 * 1024;
 
 struct StemGeom {
   int N, C, H, W, O, OH, OW;
+  int R;          // output rows per tile (4, or 2 for rows too wide for LDS)
   int n_rt;       // tiles per image
   int n_tiles;    // tiles per filter group
   int NB;         // 32-pixel blocks per tile
@@ -66,12 +65,27 @@ __device__ __forceinline__ uint32_t pack2<Bf16>(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), b2));
 }
 
+// two FP32 sums -> optional ReLU -> two rounded 16-bit values in one register; for FP16 the ReLU is one
+// v_pk_max_f16 on the rounded pair (rounding is monotonic and keeps the sign, so max(round(v), 0) ==
+// round(max(v, 0))), for BF16 the FP32 max before rounding
+template <typename E, bool RELU>
+__device__ __forceinline__ uint32_t relu2(float v0, float v1) {
+  if constexpr (RELU && E::kDtype == GIE_HIP_FP16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t,
+                              __builtin_elementwise_max(__builtin_bit_cast(h2, pack2<E>(v0, v1)), (h2){0, 0}));
+  } else {
+    if (RELU) v0 = fmaxf(v0, 0.0f), v1 = fmaxf(v1, 0.0f);
+    return pack2<E>(v0, v1);
+  }
+}
+
 template <typename E>
 constexpr uint32_t one_bits() {
   return E::kDtype == GIE_HIP_FP16 ? 0x3C00u : 0x3F80u;
 }
 
-template <typename E, int C, bool RELU>
+template <typename E, int C, int R, bool RELU>
 __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
                                                     StemGeom g) {
@@ -79,7 +93,8 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   constexpr int NG = 7 * C;             // (channel, filter row) groups
   constexpr int KS = (NG + 2) / 2;      // k-steps: NG groups + the bias group, two groups per step
   constexpr int FW = C * 49;            // weights per filter
-  constexpr int NROW = C * kStWR;       // input rows per tile
+  constexpr int WR = 2 * R + 5;         // input rows per tile and channel
+  constexpr int NROW = C * WR;          // input rows per tile
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hi = lane >> 5, col = lane & 31;
   const int og = blockIdx.x / g.G, L = blockIdx.x - og * g.G;
@@ -101,16 +116,16 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   // inactive lane writes nothing), rows above or below the image read as zeros
   auto load_rows = [&](int i) {
     const int t = t0 + i * step;
-    const int n = t / g.n_rt, oh0 = (t - n * g.n_rt) * kStR;
+    const int n = t / g.n_rt, oh0 = (t - n * g.n_rt) * R;
     unsigned char* dst = rows(i) + kStPad * 4;
     if (lane < g.CPR) {
 #pragma unroll
       for (int c = 0; c < C; ++c)
 #pragma unroll
-        for (int lr = 0; lr < kStWR; ++lr) {
+        for (int lr = 0; lr < WR; ++lr) {
           const int ih = 2 * oh0 - 3 + lr;
           const int voff = ih >= 0 && ih < g.H ? ((n * C + c) * g.H + ih) * row_bytes + lane * 16 : kOut;
-          dma16(xr, lds_addr(dst + (c * kStWR + lr) * g.RS * 4), voff);
+          dma16(xr, lds_addr(dst + (c * WR + lr) * g.RS * 4), voff);
         }
     }
   };
@@ -192,29 +207,42 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     const int grp = 2 * s + hi < NG ? 2 * s + hi : 0;
-    offs[s] = ((grp / 7) * kStWR + grp % 7) * g.RS * 4;
+    offs[s] = ((grp / 7) * WR + grp % 7) * g.RS * 4;
   }
   stage_barrier();  // tile 0's rows are in
 
-  // ---- multiplying waves: 32-pixel blocks wave, wave + 7, ... of tile i from row buffer i % 3
-  const int npix = kStR * g.OW;
+  // ---- multiplying waves: 32-pixel blocks of tile i from row buffer i % 3, in pairs (wave, wave + 7), (wave + 14,
+  // wave + 21), ...: the second block's rows are read before the first block's stores are issued
+  const int npix = R * g.OW;
+  const float inv_ow = 1.0f / float(g.OW);
+  int f_off[2];  // byte offset of the lane's filter plane in each half
+  bool f_ok[2];
+#pragma unroll
+  for (int fh = 0; fh < 2; ++fh) {
+    const int f = f0 + fh * 32 + col;
+    f_ok[fh] = f < g.O;
+    f_off[fh] = int(size_t(f_ok[fh] ? f : 0) * y_plane * 2);
+  }
   for (int i = 0; i < n_my; ++i) {
     const int t = t0 + i * step;
-    const int n = t / g.n_rt, oh0 = (t - n * g.n_rt) * kStR;
+    const int n = t / g.n_rt, oh0 = (t - n * g.n_rt) * R;
     const unsigned char* rb = rows(i);
-    for (int blk = wave; blk < g.NB; blk += kStCW) {
+    const int p_end = min(npix, (g.OH - oh0) * g.OW);  // pixels of the tile inside the image
+    const int y_tile = int((size_t(n) * g.O * y_plane + size_t(oh0) * g.OW) * 2);  // byte offset of (n, 0, oh0, 0)
+    // row dwords ow-2 .. ow+1 (input columns 2*ow-4 .. 2*ow+3) of every k-step's row: padded dwords ow+2 .. ow+5
+    auto load = [&](int blk, uint32_t (&d)[KS][4]) {
       const int p = blk * 32 + col;
       const int pc = p < npix ? p : 0;
-      const int r = pc / g.OW, ow = pc - r * g.OW;
-      // row dwords ow-2 .. ow+1 (input columns 2*ow-4 .. 2*ow+3) sit at padded dwords ow+2 .. ow+5
+      const int r = fdiv(pc, g.OW, inv_ow), ow = pc - r * g.OW;
       const unsigned char* bp = rb + (2 * r * g.RS + ow + 2) * 4;
-      uint32_t d[KS][4];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const uint32_t* q = reinterpret_cast<const uint32_t*>(bp + offs[s]);
         d[s][0] = q[0], d[s][1] = q[1], d[s][2] = q[2], d[s][3] = q[3];
       }
-      f32x16 acc0 = {0}, acc1 = {0};
+    };
+    auto multiply = [&](const uint32_t (&d)[KS][4], f32x16& acc0, f32x16& acc1) {
+      acc0 = f32x16{0}, acc1 = f32x16{0};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         // halves h0..h7 = input columns 2*ow-4 .. 2*ow+3; the group is (h1, h3, h5, h7, h2, h4, h6, 0)
@@ -231,9 +259,11 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
         acc0 = E::mfma32(b, wa[0][s], acc0);  // rows: pixels; columns: filters
         acc1 = E::mfma32(b, wa[1][s], acc1);
       }
-      // epilogue: lane (hi, col) holds filter col of the half and pixels 8a + 4hi + (0..3), a = 0..3; one
-      // v_permlane32_swap per register pair trades the lower half's a = 2, 3 for the upper half's a = 0, 1, so the
-      // lower half holds pixels 0..15 and the upper half 16..31: two 16-byte stores per lane
+    };
+    // epilogue: lane (hi, col) holds filter col of the half and pixels 8a + 4hi + (0..3), a = 0..3; one
+    // v_permlane32_swap per register pair trades the lower half's a = 2, 3 for the upper half's a = 0, 1, so the
+    // lower half holds pixels 0..15 and the upper half 16..31: two 16-byte stores per lane
+    auto store = [&](int blk, const f32x16& acc0, const f32x16& acc1) {
 #pragma unroll
       for (int fh = 0; fh < 2; ++fh) {
         const f32x16& acc = fh ? acc1 : acc0;
@@ -241,22 +271,31 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            float v0 = acc[4 * a + 2 * j], v1 = acc[4 * a + 2 * j + 1];
-            if (RELU) v0 = fmaxf(v0, 0.0f), v1 = fmaxf(v1, 0.0f);
-            P[a][j] = pack2<E>(v0, v1);
-          }
-        const int f = f0 + fh * 32 + col;
+          for (int j = 0; j < 2; ++j) P[a][j] = relu2<E, RELU>(acc[4 * a + 2 * j], acc[4 * a + 2 * j + 1]);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
           // lanes 32..63 of P[b] <-> lanes 0..31 of P[b + 2]
           const auto s0 = __builtin_amdgcn_permlane32_swap(P[b][0], P[b + 2][0], false, false);
           const auto s1 = __builtin_amdgcn_permlane32_swap(P[b][1], P[b + 2][1], false, false);
           const int p0 = blk * 32 + 16 * hi + 8 * b;  // 8 pixels of one output row (out_w % 8 == 0)
-          const bool ok = p0 < npix && oh0 + p0 / g.OW < g.OH && f < g.O;
-          const int voff = ok ? int(((size_t(n) * g.O + f) * y_plane + size_t(oh0) * g.OW + p0) * 2) : kOut;
+          const int voff = p0 < p_end && f_ok[fh] ? y_tile + f_off[fh] + p0 * 2 : kOut;
           store16(yr, voff, u32x4{s0[0], s1[0], s0[1], s1[1]});
         }
+      }
+    };
+    for (int ba = wave; ba < g.NB; ba += 2 * kStCW) {
+      const int bb = ba + kStCW;
+      uint32_t d[KS][4];
+      f32x16 acc0, acc1;
+      load(ba, d);
+      multiply(d, acc0, acc1);
+      if (bb < g.NB) {
+        load(bb, d);
+        store(ba, acc0, acc1);
+        multiply(d, acc0, acc1);
+        store(bb, acc0, acc1);
+      } else {
+        store(ba, acc0, acc1);
       }
     }
     stage_barrier();  // tile i's rows are no longer read; tile i+1's have landed
@@ -280,21 +319,27 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
   g->OH = gg->out_h, g->OW = gg->out_w;
   g->CPR = g->W / 8;
   g->RS = g->W / 2 + 2 * kStPad;
-  g->n_rt = (g->OH + kStR - 1) / kStR;
-  g->n_tiles = g->N * g->n_rt;
-  g->NB = (kStR * g->OW + 31) / 32;
-  g->G = std::max(8, std::min((g->n_tiles + 7) / 8 * 8, cus / 8 * 8));
-  g->per_xcd = (g->n_tiles + 7) / 8;
-  g->buf_bytes = g->C * kStWR * g->RS * 4;
   const int ks = (7 * g->C + 2) / 2;
   g->rows_off = (64 * g->C * 49 * 2 + 15) / 16 * 16 + 64 * ks * 2 * 16 + 128;  // weights, operands, bias
+  int R = 0;
+  for (int r : {4, 2})
+    if (g->rows_off + kStBufs * g->C * (2 * r + 5) * g->RS * 4 <= kStLdsMax) {
+      R = r;
+      break;
+    }
+  if (R == 0) return GIE_HIP_EUNSUPPORTED;
+  g->R = R;
+  g->n_rt = (g->OH + R - 1) / R;
+  g->n_tiles = g->N * g->n_rt;
+  g->NB = (R * g->OW + 31) / 32;
+  g->G = std::max(8, std::min((g->n_tiles + 7) / 8 * 8, cus / 8 * 8));
+  g->per_xcd = (g->n_tiles + 7) / 8;
+  g->buf_bytes = g->C * (2 * R + 5) * g->RS * 4;
   g->x_bytes = int(2 * nx);
   g->y_bytes = int(2 * ny);
   const long long grid = 1LL * g->G * ((g->O + 63) / 64);
   if (grid >= (1LL << 31)) return GIE_HIP_EUNSUPPORTED;
-  const int total = g->rows_off + kStBufs * g->buf_bytes;
-  if (total > kStLdsMax) return GIE_HIP_EUNSUPPORTED;
-  if (lds) *lds = total;
+  if (lds) *lds = g->rows_off + kStBufs * g->buf_bytes;
   return GIE_HIP_OK;
 }
 
@@ -308,14 +353,20 @@ int device_cus() {
 
 using StemFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, StemGeom);
 
-template <typename E, bool RELU>
+template <typename E, int R, bool RELU>
 StemFn stem_fn(int c) {
   switch (c) {
-    case 1: return &stem_kernel<E, 1, RELU>;
-    case 2: return &stem_kernel<E, 2, RELU>;
-    case 3: return &stem_kernel<E, 3, RELU>;
-    default: return &stem_kernel<E, 4, RELU>;
+    case 1: return &stem_kernel<E, 1, R, RELU>;
+    case 2: return &stem_kernel<E, 2, R, RELU>;
+    case 3: return &stem_kernel<E, 3, R, RELU>;
+    default: return &stem_kernel<E, 4, R, RELU>;
   }
+}
+
+template <typename E>
+StemFn stem_fn(int c, int r, bool relu) {
+  if (r == 4) return relu ? stem_fn<E, 4, true>(c) : stem_fn<E, 4, false>(c);
+  return relu ? stem_fn<E, 2, true>(c) : stem_fn<E, 2, false>(c);
 }
 
 }  // namespace
@@ -341,8 +392,7 @@ extern "C" int gie_hip_conv_stem(int dtype, const gie_conv_geom* gg, const void*
       (reinterpret_cast<uintptr_t>(y) & 15u))
     return GIE_HIP_EUNSUPPORTED;
   const bool bf = dtype == GIE_HIP_BF16;
-  const StemFn fn = bf ? (gg->relu ? stem_fn<Bf16, true>(g.C) : stem_fn<Bf16, false>(g.C))
-                       : (gg->relu ? stem_fn<Fp16, true>(g.C) : stem_fn<Fp16, false>(g.C));
+  const StemFn fn = bf ? stem_fn<Bf16>(g.C, g.R, gg->relu != 0) : stem_fn<Fp16>(g.C, g.R, gg->relu != 0);
   if (int rc = set_lds_limit(reinterpret_cast<const void*>(fn), lds)) return rc;
   const unsigned grid = unsigned(g.G * ((g.O + 63) / 64));
   hipLaunchKernelGGL(fn, dim3(grid), dim3(kStNT), lds, static_cast<hipStream_t>(stream),
