@@ -151,21 +151,33 @@ def _cpu_model() -> str:
 
 
 def load_traffic(kernel_name: str):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, when that summary
-    was taken on the same registry kernel (else None: counters of another tiling say nothing about this one)."""
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE scaled by a plain copy's counters), when that summary covers the same registry kernel (else None:
+    counters of another tiling say nothing about this one)."""
     path = os.path.join(ROOT, "profiles", "traffic_c2_fp16_3x3.json")
     try:
         with open(path) as f:
             d = json.load(f)
     except (OSError, ValueError):
         return None
-    return d.get("bytes_per_launch") if d.get("kernel") == kernel_name else None
+    k = d.get("kernels", {}).get(kernel_name)
+    return k.get("bytes_per_launch") if k else None
 
 
 def dominant_kernel(registry_name: str) -> str:
-    """The device function that does the implicit GEMM for a registry kernel (the rocprof kernel name)."""
-    if registry_name.startswith("halo_"):
-        return "halo_kernel (halo-tiled MFMA implicit GEMM, conv_halo.hip)"
+    """The device function that does the multiply-accumulate work for a registry kernel (the rocprof kernel name)."""
+    stems = [("band_", "band_kernel (band MFMA convolution straight from NCHW, conv_band.hip)"),
+             ("halo_", "halo_kernel (halo-tiled MFMA implicit GEMM, conv_halo.hip)"),
+             ("stem_", "stem_kernel (7x7 stride-2 stem straight from NCHW, conv_stem.hip)"),
+             ("implicit_gemm_fp32_", "f32_kernel (FP32 MFMA convolution, conv_f32.hip)"),
+             ("mfma_tf32_", "f32_kernel (TF32 MFMA convolution, conv_f32.hip)")]
+    for stem, fn in stems:
+        if registry_name.startswith(stem):
+            return fn
+    if registry_name.startswith("pw_"):
+        if registry_name.endswith("_wreg"):
+            return "pws_kernel (weight-stationary streaming pointwise, conv_pw.hip)"
+        return "pw_kernel (pointwise MFMA convolution straight from NCHW, conv_pw.hip)"
     return "igemm_kernel (MFMA implicit GEMM, conv_mfma.hip)"
 
 
