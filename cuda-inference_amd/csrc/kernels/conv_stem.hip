@@ -18,9 +18,8 @@
 //     per 32-pixel block: two ds_read2_b32 and 4 bit operations per k-step, two MFMA chains. One barrier per tile.
 //   * MFMA roles: rows = pixels, columns = filters, so each lane's accumulators hold 4-pixel runs of one filter.
 //     Epilogue: ReLU, RNE rounding (the order of the reference's apply_epilogue,
-//     src/kernels/fused_epilogue.cuh:11-16), one v_permlane32_swap per register pair so each lane holds two
-//     8-pixel runs, and 16-byte stores (one run of one filter per lane; 16-byte stores reach ~5.7 TB/s on this
-//     output where 8-byte stores of 64-byte runs stay near 3.5 TB/s).
+//     src/kernels/fused_epilogue.cuh:11-16), the wave's 64-filter x 32-pixel tile staged in LDS, 16-byte stores
+//     with every 4 lanes writing one 64-byte run of a filter's output row.
 //   * Grid: one 8-wave workgroup per CU; tiles are split into 8 contiguous ranges, one per XCD (blockIdx mod 8),
 //     so the input rows shared by neighbouring tiles are read into one L2.
 #include <algorithm>
@@ -49,6 +48,7 @@ struct StemGeom {
   int RS;         // LDS row stride in dwords: in_w / 2 + 8
   int buf_bytes;  // one row buffer: C * WR * RS * 4
   int rows_off;   // LDS byte offset of the row buffers (after the prologue's weights)
+  int tile_off;   // LDS byte offset of the multiplying waves' output tiles (4 KiB each)
   int x_bytes, y_bytes;
 };
 
@@ -215,13 +215,27 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   // wave + 21), ...: the second block's rows are read before the first block's stores are issued
   const int npix = R * g.OW;
   const float inv_ow = 1.0f / float(g.OW);
-  int f_off[2];  // byte offset of the lane's filter plane in each half
-  bool f_ok[2];
+  // Output tile of this wave in LDS: row r (64 bytes) holds filter f0 + r; its 8-byte granule q sits at
+  // q ^ (2 * ((r / 4) & 3)). Writes: lane (hi, col) puts pixels 8a + 4hi .. +3 of filter 32fh + col into granule
+  // 2a + hi of row 32fh + col. Reads: read t of lane l covers row 16t + l/4, 16-byte segment l%4 (stored at
+  // segment (l%4) ^ ((l/16) & 3)).
+  typedef __attribute__((address_space(3))) u32x2 lds_u32x2_t;
+  typedef __attribute__((address_space(3))) const u32x4 lds_cu32x4_t;
+  const unsigned stg = lds_addr(smem + g.tile_off) + unsigned(wave) * 4096u;
+  lds_u32x2_t* w_q[4];
 #pragma unroll
-  for (int fh = 0; fh < 2; ++fh) {
-    const int f = f0 + fh * 32 + col;
-    f_ok[fh] = f < g.O;
-    f_off[fh] = int(size_t(f_ok[fh] ? f : 0) * y_plane * 2);
+  for (int a = 0; a < 4; ++a)
+    w_q[a] = reinterpret_cast<lds_u32x2_t*>(size_t(
+        stg + unsigned(col) * 64u + (((unsigned(a) ^ ((unsigned(lane) >> 2) & 3u)) << 1 | unsigned(hi)) << 3)));
+  lds_cu32x4_t* const r_base = reinterpret_cast<lds_cu32x4_t*>(
+      size_t(stg + (unsigned(lane) >> 2) * 64u + (((unsigned(lane) & 3u) ^ ((unsigned(lane) >> 4) & 3u)) << 4)));
+  int f_off[4];  // byte offset of the filter plane of each read's row
+  bool f_ok[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int f = f0 + 16 * t + (lane >> 2);
+    f_ok[t] = f < g.O;
+    f_off[t] = int(size_t(f_ok[t] ? f : 0) * y_plane * 2);
   }
   for (int i = 0; i < n_my; ++i) {
     const int t = t0 + i * step;
@@ -260,27 +274,29 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
         acc1 = E::mfma32(b, wa[1][s], acc1);
       }
     };
-    // epilogue: lane (hi, col) holds filter col of the half and pixels 8a + 4hi + (0..3), a = 0..3; one
-    // v_permlane32_swap per register pair trades the lower half's a = 2, 3 for the upper half's a = 0, 1, so the
-    // lower half holds pixels 0..15 and the upper half 16..31: two 16-byte stores per lane
+    // epilogue: lane (hi, col) holds filter col of each 32-filter half and pixels 8a + 4hi + (0..3), a = 0..3.
+    // ReLU and the rounding in registers, then the wave's 64 x 32 tile goes through its own 4 KiB of LDS so that
+    // every 4 lanes write one 64-byte run of a filter's output row (16 runs per store instruction; measured
+    // faster than 16-byte runs of 32 filters per instruction straight from the registers).
     auto store = [&](int blk, const f32x16& acc0, const f32x16& acc1) {
 #pragma unroll
       for (int fh = 0; fh < 2; ++fh) {
         const f32x16& acc = fh ? acc1 : acc0;
-        uint32_t P[4][2];
 #pragma unroll
         for (int a = 0; a < 4; ++a)
+          w_q[a][fh * 256] = u32x2{relu2<E, RELU>(acc[4 * a], acc[4 * a + 1]), relu2<E, RELU>(acc[4 * a + 2], acc[4 * a + 3])};
+      }
+      // the tile is written as 8-byte and read as 16-byte vectors: keep the compiler from reordering them (the
+      // wave's LDS accesses complete in issue order)
+      asm volatile("" ::: "memory");
+      u32x4 v[4];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) P[a][j] = relu2<E, RELU>(acc[4 * a + 2 * j], acc[4 * a + 2 * j + 1]);
+      for (int t = 0; t < 4; ++t) v[t] = r_base[t * 64];
+      const int p0 = blk * 32 + 8 * (lane & 3);  // the lane's 8 pixels of one output row (out_w % 8 == 0)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          // lanes 32..63 of P[b] <-> lanes 0..31 of P[b + 2]
-          const auto s0 = __builtin_amdgcn_permlane32_swap(P[b][0], P[b + 2][0], false, false);
-          const auto s1 = __builtin_amdgcn_permlane32_swap(P[b][1], P[b + 2][1], false, false);
-          const int p0 = blk * 32 + 16 * hi + 8 * b;  // 8 pixels of one output row (out_w % 8 == 0)
-          const int voff = p0 < p_end && f_ok[fh] ? y_tile + f_off[fh] + p0 * 2 : kOut;
-          store16(yr, voff, u32x4{s0[0], s1[0], s0[1], s1[1]});
-        }
+      for (int t = 0; t < 4; ++t) {
+        const int voff = p0 < p_end && f_ok[t] ? y_tile + f_off[t] + p0 * 2 : kOut;
+        store16(yr, voff, v[t]);
       }
     };
     for (int ba = wave; ba < g.NB; ba += 2 * kStCW) {
@@ -323,7 +339,7 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
   g->rows_off = (64 * g->C * 49 * 2 + 15) / 16 * 16 + 64 * ks * 2 * 16 + 128;  // weights, operands, bias
   int R = 0;
   for (int r : {4, 2})
-    if (g->rows_off + kStBufs * g->C * (2 * r + 5) * g->RS * 4 <= kStLdsMax) {
+    if (g->rows_off + kStBufs * g->C * (2 * r + 5) * g->RS * 4 + kStCW * 4096 <= kStLdsMax) {
       R = r;
       break;
     }
@@ -339,7 +355,8 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
   g->y_bytes = int(2 * ny);
   const long long grid = 1LL * g->G * ((g->O + 63) / 64);
   if (grid >= (1LL << 31)) return GIE_HIP_EUNSUPPORTED;
-  if (lds) *lds = g->rows_off + kStBufs * g->buf_bytes;
+  g->tile_off = g->rows_off + kStBufs * g->buf_bytes;
+  if (lds) *lds = g->tile_off + kStCW * 4096;
   return GIE_HIP_OK;
 }
 

@@ -3,7 +3,7 @@ NCHW) through its C-ABI and through the registry entries, against the oracle's d
 reference's tolerance (tests/conv_test_common.h:83-127).
 
 Cases cover every channel count 1..4, filter counts below, at and over one 64-filter group, odd output heights
-(the last 2-row tile holds one valid row), widths from 16 to the widest that fit (480 with 4 channels, 512), fewer tiles than workgroups, no bias / no ReLU, both precisions, a second launch overwriting the first
+(the last 2-row tile holds one valid row), widths from 16 to the widest that fit (336 with 4 channels, 512), fewer tiles than workgroups, no bias / no ReLU, both precisions, a second launch overwriting the first
 with the same bits, BASELINE config 4 (N64 C3 224x224 K64) at full size (sampled outputs + the benchmark gates),
 caller tensors that are only 2-byte aligned (the entry runs the implicit-GEMM fallback) and argument rejection.
 """
@@ -30,7 +30,7 @@ CASES = [
     (3, 2, 17, 32, 70, "fp16", True, True),       # C = 2, odd output height, two filter groups
     (2, 4, 40, 48, 128, "bf16", False, True),     # C = 4, no bias
     (1, 3, 9, 16, 64, "fp16", True, True),        # smallest width: out_w 8, three tiles only
-    (1, 4, 6, 480, 64, "fp16", True, True),       # widest rows that fit LDS with C = 4 (480 columns)
+    (1, 4, 6, 336, 64, "fp16", True, True),       # widest rows that fit LDS with C = 4 (336 columns)
     (1, 3, 4, 512, 64, "bf16", True, True),       # widest rows (512 columns)
     (4, 3, 64, 64, 32, "bf16", True, True),       # filter count 32
     (2, 3, 30, 48, 64, "fp16", False, False),     # no epilogue
@@ -66,7 +66,7 @@ def test_stem_geometry_and_argument_checks():
                 gie.Problem(2, 3, 32, 32, 64, 7, 7, 2, 2, 2, 2, precision="fp16"),   # padding 2
                 _problem(2, 5, 32, 32, 64, "fp16", True, True),                     # C = 5
                 _problem(2, 3, 32, 40, 64, "fp16", True, True),                     # in_w % 16 != 0
-                _problem(1, 4, 6, 496, 64, "fp16", True, True),                     # rows too wide for LDS
+                _problem(1, 4, 6, 352, 64, "fp16", True, True),                     # rows too wide for LDS
                 _problem(1, 3, 6, 528, 64, "fp16", True, True)):                    # rows over 512 columns
         assert h.gie_hip_stem_check(ctypes.byref(bad.geom(bad.in_channels)), None) != 0
     ok = _problem(2, 3, 32, 32, 64, "fp16", True, True)
