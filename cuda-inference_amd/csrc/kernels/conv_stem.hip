@@ -147,19 +147,19 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   constexpr int kFragBytes = 64 * KS * 2 * 16;
   u32x4* frag = reinterpret_cast<u32x4*>(smem + kWBytes);
   uint16_t* bl = reinterpret_cast<uint16_t*>(smem + kWBytes + kFragBytes);
-  {
-    constexpr int kW16 = (64 * FW * 2 / 16 + kStNT - 1) / kStNT;  // 16-byte chunks per thread
+  if (wave != kStLoader) {  // (the streaming wave keeps its vector-memory counter to the row loads)
+    constexpr int kMT = kStCW * 64;                               // threads of the multiplying waves
+    constexpr int kW16 = (64 * FW * 2 / 16 + kMT - 1) / kMT;      // 16-byte chunks per thread
     const int nh = nf * FW, n16 = nh >> 3;
     const u32x4* w16 = reinterpret_cast<const u32x4*>(w + size_t(f0) * FW);
     u32x4 tmp[kW16];
 #pragma unroll
-    for (int k = 0; k < kW16; ++k)
-      if (tid + k * kStNT < n16) tmp[k] = w16[tid + k * kStNT];
+    for (int k = 0; k < kW16; ++k) tmp[k] = w16[min(tid + k * kMT, n16 - 1)];  // all loads in flight at once
     if (tid < nh - n16 * 8) wl[n16 * 8 + tid] = w[size_t(f0) * FW + n16 * 8 + tid];
     if (tid < nf) bl[tid] = bias != nullptr ? bias[f0 + tid] : uint16_t(0);
 #pragma unroll
     for (int k = 0; k < kW16; ++k)
-      if (tid + k * kStNT < n16) *reinterpret_cast<u32x4*>(wl + (tid + k * kStNT) * 8) = tmp[k];
+      if (tid + k * kMT < n16) *reinterpret_cast<u32x4*>(wl + (tid + k * kMT) * 8) = tmp[k];
   }
   __syncthreads();
   // operand (filter f, k-step s, half h) = 8 halves of group 2s + h: kw 0, 2, 4, 6, 1, 3, 5, 0; the bias group
@@ -182,7 +182,8 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   if (wave == kStLoader) {
     // ---- streaming wave: before the barrier that ends tile i, tile i+1's rows must have landed; tile i+2's are
     // issued first and may stay in flight (this wave issues no other vector-memory operation in the loop)
-    wait_vm<0>();  // tile 0's rows (the weight loads above were waited for, and issued after them)
+    if (n_my > 1) wait_vm<NROW>();  // tile 0's rows are in; tile 1's may be in flight
+    else wait_vm<0>();
     stage_barrier();
     for (int i = 0; i < n_my; ++i) {
       if (i + 2 < n_my) {
