@@ -107,6 +107,26 @@ __global__ __launch_bounds__(kThreads) void repack_blocked_kernel(BlockedJob j) 
   else weight_filter(j, int(blk - j.n_act), buf);
 }
 
+// Weights only, one thread per 16-byte output vector (filter o, slice s, tap rs, 8-channel group k): its 8
+// halves w[o][s*32 + 8k + j][rs] are gathered straight from global memory (all 8 loads in flight, no LDS
+// round trip or barrier: the weight repack sits on the critical path of every band call).
+__global__ __launch_bounds__(kThreads) void repack_w_direct_kernel(const uint16_t* __restrict__ w,
+                                                                  uint16_t* __restrict__ wb, int C, int RS,
+                                                                  int S, long long n_vec) {
+  const long long q = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (q >= n_vec) return;
+  const int per_o = S * RS * 4;
+  const int o = int(q / per_o), r = int(q - static_cast<long long>(o) * per_o);
+  const int k = r & 3, tr = r >> 2, s = tr / RS, rs = tr - s * RS;
+  const int c0 = s * 32 + k * 8;
+  const uint16_t* src = w + (static_cast<long long>(o) * C + c0) * RS + rs;
+  uint32_t h[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = c0 + j < C ? uint32_t(src[j * RS]) : 0u;
+  *reinterpret_cast<u32x4*>(wb + q * 8) = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                                h[6] | (h[7] << 16)};
+}
+
 }  // namespace
 }  // namespace gie_hip
 
@@ -157,5 +177,18 @@ extern "C" int gie_hip_repack_blocked(const void* x, void* xb, const void* w, vo
 }
 
 extern "C" int gie_hip_repack_w_blocked(const void* w, void* wb, const gie_conv_geom* g, void* stream) {
-  return repack_blocked(nullptr, nullptr, w, wb, g, stream);
+  if (!g || !w || !wb) return GIE_HIP_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(wb) & 15u) || (reinterpret_cast<uintptr_t>(w) & 1u)) return GIE_HIP_EINVAL;
+  if (g->in_channels <= 0 || g->out_channels <= 0 || g->kernel_h <= 0 || g->kernel_w <= 0) return GIE_HIP_EINVAL;
+  const long long rs = static_cast<long long>(g->kernel_h) * g->kernel_w;
+  const int S = (g->in_channels + 31) / 32;
+  const long long n_vec = static_cast<long long>(g->out_channels) * S * rs * 4;
+  if (rs * g->in_channels > 0x7fffffffLL || S * rs * 4 > 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
+  const long long blocks = (n_vec + kThreads - 1) / kThreads;
+  if (blocks > 0x7fffffffLL) return GIE_HIP_EUNSUPPORTED;
+  hipLaunchKernelGGL(repack_w_direct_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), static_cast<uint16_t*>(wb),
+                     g->in_channels, int(rs), S, n_vec);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GIE_HIP_OK : int(e);
 }
