@@ -184,6 +184,8 @@ _HIP = {
     "gie_hip_conv_pws": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_stem_check": ([_GP, _vp], _i),
     "gie_hip_conv_stem": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
+    "gie_hip_narrow_check": ([_GP, _vp], _i),
+    "gie_hip_conv_narrow": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_f32_config_count": ([], _i),
     "gie_hip_f32_config_tile_m": ([_i], _i),
     "gie_hip_f32_check": ([_i, _GP, _vp], _i),

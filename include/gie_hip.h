@@ -24,6 +24,7 @@
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
  *   gie_hip_conv_pws, _pws_check     the same, weight-stationary streaming form for in_channels <= 256
  *   gie_hip_conv_stem, _stem_check   transposes + tcmma_kernel for the 7x7 stride-2 stem (in_channels <= 4), fused
+ *   gie_hip_conv_narrow, _narrow_check transposes + tcmma_kernel (+ split-K reduce) for 3x3 layers with few pixels
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
  *   gie_hip_conv_f32, _f32_check     implicit_gemm_kernel<<<>>> launch (FP32) and the TF32 path
  *                                                                         src/kernels/implicit_gemm.cu:47-189,204-214
@@ -200,6 +201,15 @@ int gie_hip_conv_pws(int dtype, const gie_conv_geom* g, const void* x, const voi
 int gie_hip_stem_check(const gie_conv_geom* g, int* lds_bytes);
 int gie_hip_conv_stem(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
                       void* stream);
+
+/* Narrow convolution straight from NCHW x / OIHW w for 3x3, stride 1, padding 1 layers with in_channels % 128 == 0
+   whose 32-pixel blocks touch few enough images to stage them in LDS (the whole reduction in one workgroup, no
+   partials): fused bias + ReLU, dtype GIE_HIP_FP16 / _BF16 (x and w 16-byte aligned, y and bias 2-byte aligned;
+   GIE_HIP_EUNSUPPORTED for other alignments or geometries). One launch, no workspace. *_check: 0 when the
+   geometry qualifies, LDS bytes per workgroup in *lds_bytes. */
+int gie_hip_narrow_check(const gie_conv_geom* g, int* lds_bytes);
+int gie_hip_conv_narrow(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
+                        void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
    dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */

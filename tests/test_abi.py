@@ -148,3 +148,15 @@ def test_stem_geometry_check_on_host():
               gie.Problem(1, 4, 6, 352, 64, 7, 7, 2, 2, 3, 3, precision="fp16"),
               gie.Problem(1, 3, 6, 528, 64, 7, 7, 2, 2, 3, 3, precision="fp16")):
         assert gie.hip().gie_hip_stem_check(ctypes.byref(p.geom(p.in_channels)), None) != 0
+
+
+def test_narrow_geometry_check_on_host():
+    """gie_hip_narrow_check is host arithmetic: the GPU narrow tests' shapes qualify within the LDS limit."""
+    for B, C, H, W, K in [(2, 128, 5, 5, 40), (3, 256, 4, 4, 64), (1, 128, 14, 14, 96), (40, 128, 1, 1, 20),
+                          (8, 512, 7, 7, 512), (2, 384, 6, 6, 33)]:
+        p = gie.Problem(B, C, H, W, K, 3, 3, 1, 1, 1, 1, precision="bf16")
+        lds = ctypes.c_int(0)
+        assert gie.hip().gie_hip_narrow_check(ctypes.byref(p.geom(C)), ctypes.byref(lds)) == 0, (B, C, H, W, K)
+        assert 0 < lds.value <= 160 * 1024
+    p = gie.Problem(2, 1024, 56, 56, 64, 3, 3, 1, 1, 1, 1, precision="fp16")
+    assert gie.hip().gie_hip_narrow_check(ctypes.byref(p.geom(1024)), None) != 0
