@@ -9,8 +9,9 @@
 //     a k-step are one 16-byte load straight from w (no repack);
 //   * the activations of the images the block touches (at most a few, C x H x W each) are copied to LDS once; the
 //     pixel operand (8 consecutive k = (channel, tap) pairs of the lane's pixel) is gathered from there with
-//     per-lane tables built once: for each of the 9 k-steps of a 16-channel unit, the offset of every element
-//     relative to the unit's first channel and whether the tap falls in the padding;
+//     tables built once per workgroup in LDS and held in registers: for each of the 9 k-steps of a 16-channel
+//     unit, the offset of every element relative to the unit's first channel, and per element pair a mask that
+//     zeroes the taps in the padding;
 //   * the 8 waves split the channels (C / 8 each, in 16-channel units), then the 8 partial tiles are summed in LDS
 //     in wave order (deterministic) and the sum gets bias + ReLU and one RNE rounding (the order of the
 //     reference's apply_epilogue, src/kernels/fused_epilogue.cuh:11-16).
@@ -29,10 +30,12 @@ constexpr int kNaLdsMax = 160 * 1024;
 
 struct NarrowGeom {
   int B, C, H, W, O, HW, NPIX, K;
+  int x_bytes;
   int n_pb;      // 32-pixel blocks
   int n_tiles;   // filter blocks x pixel blocks
   int per_xcd;   // tiles per XCD range
   int cw;        // channels per wave (a multiple of 16)
+  int tab_off;   // LDS byte offset of the gather tables (after the staged activations)
 };
 
 template <typename E, bool RELU>
@@ -51,72 +54,89 @@ __global__ __launch_bounds__(kNaNT) void narrow_kernel(const uint16_t* __restric
   // ---- the activations of the images this pixel block touches, one contiguous NCHW range, into LDS
   const int img_lo = p0 / g.HW;
   const int img_hi = min(p0 + 31, g.NPIX - 1) / g.HW;
+  // (buffer_load ... lds: 64 chunks of 16 bytes per instruction, all in flight at once; lanes past the range are
+  // inactive and write nothing)
   {
     const int n16 = (img_hi - img_lo + 1) * g.C * g.HW / 8;  // C % 128 == 0: whole 16-byte chunks
-    const u32x4* src = reinterpret_cast<const u32x4*>(x + size_t(img_lo) * g.C * g.HW);
-    u32x4* dst = reinterpret_cast<u32x4*>(smem);
-    for (int i0 = tid; i0 < n16; i0 += 4 * kNaNT) {
-      u32x4 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = src[min(i0 + u * kNaNT, n16 - 1)];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (i0 + u * kNaNT < n16) dst[i0 + u * kNaNT] = v[u];
+    const v4i xr = make_vsharp(x, g.x_bytes);
+    const int src0 = img_lo * g.C * g.HW * 2;
+    for (int j = wave; j * 64 < n16; j += kNaWaves) {
+      const int ci = j * 64 + lane;
+      if (ci < n16) dma16(xr, lds_addr(smem + j * 1024), src0 + ci * 16);
     }
+    wait_vmcnt<0>();
   }
 
-  // ---- per-lane gather tables: element j of k-step s of a 16-channel unit is k = 16s + 8hi + j of the unit,
-  // channel k / 9, tap k % 9; its LDS offset (halves) relative to the unit's first channel, and a valid bit (the
-  // tap is inside the image)
-  const int p = p0 + col;
-  const int pc = p < g.NPIX ? p : p0;
-  const int img = pc / g.HW, q = pc - img * g.HW;
-  const int oh = q / g.W, ow = q - oh * g.W;
-  const int lbase = (img - img_lo) * g.C * g.HW;
-  int off[9];
-  unsigned tap_ok = 0;
+  // ---- gather tables, built once per workgroup in LDS (every wave multiplies the same 32 pixels): element j of
+  // k-step s of a 16-channel unit is k = 16s + 8hi + j of the unit, channel k / 9, tap k % 9. For lane (hi, col):
+  // its LDS offset (halves) relative to the unit's first channel of the lane's image, and per element pair a
+  // mask that zeroes the taps in the padding.
+  int* tab_rel = reinterpret_cast<int*>(smem + g.tab_off);                 // [hi][col][72]
+  uint8_t* tab_ok = smem + g.tab_off + 2 * 32 * 72 * 4;                     // [hi][col][72]
+  uint32_t* tab_msk = reinterpret_cast<uint32_t*>(smem + g.tab_off + 2 * 32 * 72 * 5);  // [hi][col][36]
+  {
+    const int th = tid >> 8, tc = (tid >> 3) & 31, part = tid & 7;
+    const int p = p0 + tc;
+    const int pc = p < g.NPIX ? p : p0;
+    const int img = pc / g.HW, q = pc - img * g.HW;
+    const int oh = q / g.W, ow = q - oh * g.W;
+    const int lbase = (img - img_lo) * g.C * g.HW;
 #pragma unroll
-  for (int tp = 0; tp < 9; ++tp) {
-    const int ih = oh + tp / 3 - 1, iw = ow + tp % 3 - 1;
-    const bool ok = ih >= 0 && ih < g.H && iw >= 0 && iw < g.W;
-    off[tp] = ok ? ih * g.W + iw : 0;
-    tap_ok |= (ok ? 1u : 0u) << tp;
-  }
-  int rel[9][8];
-  unsigned vbits[3] = {0u, 0u, 0u};
-#pragma unroll
-  for (int s = 0; s < 9; ++s)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int ka = 16 * s + j, kb = 16 * s + 8 + j;  // the lane's k for hi = 0 and hi = 1
-      const int ra = (ka / 9) * g.HW + off[ka % 9], rb = (kb / 9) * g.HW + off[kb % 9];
-      const bool va = (tap_ok >> (ka % 9)) & 1u, vb = (tap_ok >> (kb % 9)) & 1u;
-      rel[s][j] = hi ? rb : ra;
-      const int e = s * 8 + j;
-      vbits[e >> 5] |= ((hi ? vb : va) ? 1u : 0u) << (e & 31);
+    for (int u = 0; u < 9; ++u) {
+      const int e = part * 9 + u, k = 16 * (e >> 3) + 8 * th + (e & 7);
+      const int c = k / 9, tp = k - c * 9;
+      const int ih = oh + tp / 3 - 1, iw = ow + tp % 3 - 1;
+      const bool ok = ih >= 0 && ih < g.H && iw >= 0 && iw < g.W;
+      tab_rel[(th * 32 + tc) * 72 + e] = lbase + c * g.HW + (ok ? ih * g.W + iw : 0);
+      tab_ok[(th * 32 + tc) * 72 + e] = ok ? 1 : 0;
     }
+  }
+  __syncthreads();  // (also: the activations are in)
+  for (int i = tid; i < 2 * 32 * 36; i += kNaNT) {
+    const int lc = i / 36, pr = i - lc * 36;
+    tab_msk[i] = (tab_ok[lc * 72 + 2 * pr] ? 0xffffu : 0u) | (tab_ok[lc * 72 + 2 * pr + 1] ? 0xffff0000u : 0u);
+  }
   __syncthreads();
+  int rel[72];
+  uint32_t msk[36];
+  {
+    const u32x4* tr = reinterpret_cast<const u32x4*>(tab_rel + (hi * 32 + col) * 72);
+    const u32x4* tm = reinterpret_cast<const u32x4*>(tab_msk + (hi * 32 + col) * 36);
+#pragma unroll
+    for (int v = 0; v < 18; ++v) {
+      const u32x4 r = tr[v];
+      rel[4 * v] = int(r.x), rel[4 * v + 1] = int(r.y), rel[4 * v + 2] = int(r.z), rel[4 * v + 3] = int(r.w);
+    }
+#pragma unroll
+    for (int v = 0; v < 9; ++v) {
+      const u32x4 m = tm[v];
+      msk[4 * v] = m.x, msk[4 * v + 1] = m.y, msk[4 * v + 2] = m.z, msk[4 * v + 3] = m.w;
+    }
+  }
 
   // ---- this wave's channels [wave * cw, +cw) in units of 16: 9 k-steps of 16 each
   const uint16_t* xl = reinterpret_cast<const uint16_t*>(smem);
   const uint16_t* wrow = w + size_t(min(f0 + col, g.O - 1)) * g.K + 8 * hi;  // rows past O: any valid row
   f32x16 acc = {0};
   const int c_beg = wave * g.cw;
-  for (int cu = c_beg; cu < c_beg + g.cw; cu += 16) {
-    u32x4 a[9];
+  // the next unit's weights are loaded while this unit is multiplied
+  u32x4 a[9], an[9];
 #pragma unroll
-    for (int s = 0; s < 9; ++s) a[s] = *reinterpret_cast<const u32x4*>(wrow + cu * 9 + 16 * s);
-    const uint16_t* xu = xl + lbase + cu * g.HW;
+  for (int s = 0; s < 9; ++s) an[s] = *reinterpret_cast<const u32x4*>(wrow + c_beg * 9 + 16 * s);
+  for (int cu = c_beg; cu < c_beg + g.cw; cu += 16) {
+#pragma unroll
+    for (int s = 0; s < 9; ++s) a[s] = an[s];
+    const int cn = cu + 16 < c_beg + g.cw ? cu + 16 : cu;  // past the last unit: reload this one (any valid row)
+#pragma unroll
+    for (int s = 0; s < 9; ++s) an[s] = *reinterpret_cast<const u32x4*>(wrow + cn * 9 + 16 * s);
+    const uint16_t* xu = xl + cu * g.HW;
 #pragma unroll
     for (int s = 0; s < 9; ++s) {
       uint32_t h[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int e = s * 8 + j;
-        const uint32_t v = xu[rel[s][j]];
-        h[j] = ((vbits[e >> 5] >> (e & 31)) & 1u) ? v : 0u;
-      }
-      const u32x4 b = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      for (int j = 0; j < 8; ++j) h[j] = xu[rel[s * 8 + j]];
+      const u32x4 b = u32x4{(h[0] | (h[1] << 16)) & msk[4 * s], (h[2] | (h[3] << 16)) & msk[4 * s + 1],
+                            (h[4] | (h[5] << 16)) & msk[4 * s + 2], (h[6] | (h[7] << 16)) & msk[4 * s + 3]};
       acc = E::mfma32(a[s], b, acc);  // rows: filters; columns: pixels
     }
   }
@@ -154,12 +174,13 @@ int narrow_prepare(const gie_conv_geom* gg, NarrowGeom* g, int* lds) {
   const long long hw = 1LL * gg->in_h * gg->in_w;
   const long long npix = gg->batch * hw;
   if (npix >= (1LL << 24) || 1LL * gg->out_channels * gg->in_channels * 9 >= (1LL << 31) ||
-      npix * gg->in_channels >= (1LL << 31) || npix * gg->out_channels >= (1LL << 31))
+      2 * npix * gg->in_channels >= (1LL << 31) || npix * gg->out_channels >= (1LL << 31))
     return GIE_HIP_EUNSUPPORTED;
   // images one 32-pixel block can touch, staged whole in LDS
   const long long n_img = std::min<long long>(gg->batch, 31 / hw + 2);
-  const long long x_lds = n_img * gg->in_channels * hw * 2;
-  const long long need = std::max<long long>(x_lds, kNaWaves * 16 * 64 * 4);
+  const long long x_lds = (n_img * gg->in_channels * hw * 2 + 15) / 16 * 16;
+  const long long tab = 2 * 32 * 72 * 5 + 2 * 32 * 36 * 4;  // offsets, valid flags, pair masks
+  const long long need = std::max<long long>(x_lds + tab, kNaWaves * 16 * 64 * 4);
   if (need > kNaLdsMax) return GIE_HIP_EUNSUPPORTED;
   g->B = gg->batch, g->C = gg->in_channels, g->H = gg->in_h, g->W = gg->in_w, g->O = gg->out_channels;
   g->HW = int(hw), g->NPIX = int(npix), g->K = gg->in_channels * 9;
@@ -167,6 +188,8 @@ int narrow_prepare(const gie_conv_geom* gg, NarrowGeom* g, int* lds) {
   g->n_tiles = (g->O + 31) / 32 * g->n_pb;
   g->per_xcd = (g->n_tiles + 7) / 8;
   g->cw = g->C / kNaWaves;
+  g->tab_off = int(x_lds);
+  g->x_bytes = int(npix * gg->in_channels * 2);
   if (lds) *lds = int(need);
   return GIE_HIP_OK;
 }
