@@ -1,5 +1,6 @@
-// Load-pipeline vocabulary shared by the LDS-staged MFMA kernels (conv_halo.hip, conv_band.hip): buffer resources,
-// direct-to-LDS loads, counted waits and the barrier that does not drain prefetches. Private to csrc/kernels.
+// Load-pipeline vocabulary shared by the LDS-staged MFMA kernels (conv_halo, conv_band, conv_pw, conv_stem,
+// conv_narrow): buffer resources, direct-to-LDS loads, inline-assembly loads and stores that the kernels count
+// themselves, counted waits and the barrier that does not drain prefetches. Private to csrc/kernels.
 #pragma once
 
 #include <mutex>

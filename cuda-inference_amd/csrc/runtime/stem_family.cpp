@@ -72,7 +72,7 @@ struct Fns {
   }
   static int64_t blocks(const ConvProblem& prob) {  // persistent: one workgroup per CU and 64-filter group
     const Conv2DParams& p = prob.p;
-    const int64_t tiles = int64_t(p.batch) * ((p.out_h() + 1) / 2);
+    const int64_t tiles = int64_t(p.batch) * ((p.out_h() + 3) / 4);  // 4-row tiles (2 for wide rows)
     return std::min<int64_t>((tiles + 7) / 8 * 8, 256) * ((p.out_channels + 63) / 64);
   }
   static double extra_traffic(const ConvProblem&) { return 0.0; }  // X, W read and Y written once from HBM
