@@ -117,3 +117,12 @@ def test_bench_config4_full_size():
     gates = b.gates(y)
     assert m.passed(), f"{k}: {m.summary()}"
     assert gates["rel_l2"] <= 1e-3 and gates["max_abs"] <= 2e-2, f"{k}: {gates}"
+
+
+def test_dispatcher_routes_config4_to_the_stem_entry():
+    """The cost model alone (no tuning) picks the stem entry for BASELINE config 4."""
+    c = dict(BENCH_CONFIGS["c4_fp16_7x7s2"])
+    prec = c.pop("precision")
+    p = gie.Problem(**c, precision=prec, has_bias=True, relu=True)
+    k, src, _ = gie.select(p)
+    assert k == "stem_fp16_7x7s2_64x32x16_wreg" and src == "cost_model", (k, src)
