@@ -169,6 +169,7 @@ def dominant_kernel(registry_name: str) -> str:
     stems = [("band_", "band_kernel (band MFMA convolution straight from NCHW, conv_band.hip)"),
              ("halo_", "halo_kernel (halo-tiled MFMA implicit GEMM, conv_halo.hip)"),
              ("stem_", "stem_kernel (7x7 stride-2 stem straight from NCHW, conv_stem.hip)"),
+             ("narrow_", "narrow_kernel (3x3, whole reduction per workgroup, conv_narrow.hip)"),
              ("implicit_gemm_fp32_", "f32_kernel (FP32 MFMA convolution, conv_f32.hip)"),
              ("mfma_tf32_", "f32_kernel (TF32 MFMA convolution, conv_f32.hip)")]
     for stem, fn in stems:
