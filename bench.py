@@ -166,7 +166,8 @@ def load_traffic(kernel_name: str):
 
 def dominant_kernel(registry_name: str) -> str:
     """The device function that does the multiply-accumulate work for a registry kernel (the rocprof kernel name)."""
-    stems = [("band_", "band_kernel (band MFMA convolution straight from NCHW, conv_band.hip)"),
+    stems = [("slab_", "slab_kernel (3x3 MFMA convolution straight from NCHW / OIHW, conv_slab.hip)"),
+             ("band_", "band_kernel (band MFMA convolution straight from NCHW, conv_band.hip)"),
              ("halo_", "halo_kernel (halo-tiled MFMA implicit GEMM, conv_halo.hip)"),
              ("stem_", "stem_kernel (7x7 stride-2 stem straight from NCHW, conv_stem.hip)"),
              ("narrow_", "narrow_kernel (3x3, whole reduction per workgroup, conv_narrow.hip)"),

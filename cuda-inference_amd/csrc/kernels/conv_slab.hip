@@ -1,0 +1,775 @@
+// Slab convolution: 3x3 filter, stride 1, padding 1, straight from NCHW x and OIHW w on gfx950 matrix cores
+// (v_mfma_f32_16x16x32_{f16,bf16}, FP32 accumulation). One launch; no repack and no workspace (split 1).
+//
+// A workgroup owns 32 output channels x one slab of RB output rows of one image. In LDS the slab's input rows
+// (one halo row above and below) form a flat array of positions, P per row (P >= in_w + 1): input (ih, iw) sits at
+// position q = (ih - oh0 + 1) * P + iw, and positions in_w .. P-1 of every row are zero (they are both the right
+// padding of the row and, seen from the next row, its left padding). Output pixel (oh, ow) has the flat index
+// o = (oh - oh0) * P + ow, and tap (r, s) of it reads position o + r * P + s - 1. A 16 x 16 MFMA block is 16
+// consecutive flat outputs, so the pixel operand of tap row r is one 16-position read at o + r * P for all three
+// tap columns, and the tap column enters through three accumulator sets:
+//     acc_s[o] = sum_r W[r][s] . X[o + r*P],     y[o] = acc_0[o - 1] + acc_1[o] + acc_2[o + 1],
+// the shifts being DPP lane moves applied once in the epilogue (flat outputs at columns >= in_w are dropped; an
+// accumulator just outside a wave's rows only ever reads padding columns and counts as zero). The inner loop is
+// LDS reads, 36 v_perm per slice and MFMAs.
+//
+// Waves: (filter half fh: 16 filters) x (row half wr: RW = 16 * NBW / P rows = NBW blocks) x (channel half kh,
+// NWK = 2 only: the two 32-channel halves of a 64-channel slice, waves w and w + 4, which share a SIMD and whose
+// sums meet in LDS at the end).
+//
+// Both operands travel by direct-to-LDS loads (no registers), NST stages, one slice in flight per stage:
+//   * weights: each filter's OIHW run of the slice (CS x 9 contiguous halves) by 16-byte loads into a staging row
+//     of CS*18 + 16 bytes (the extra 16 bytes spread the rows over the banks). A wave reads its lanes' 144-byte runs
+//     (8 channels x 9 taps of one filter) with 9 ds_read_b128 and transposes them in registers (v_perm) into the 9
+//     tap fragments (8 channels of one tap per lane) — there is no weight repack anywhere;
+//   * activations: 4-byte loads place every channel's input rows at their padded positions directly ([channel][32-
+//     byte segments of 16 positions], segment slot = segment ^ swizzle(channel) so the transposing fragment reads
+//     of 8 channels hit 8 distinct bank groups); out-of-image rows and padding columns load as zeros, so nothing is
+//     ever cleared. The pixel fragments come out with ds_read_b64_tr_b16 (4 channels of 16 positions per 16-lane
+//     group, each lane receiving the 4 channels of its position). Rows of odd width (or x not 4-byte aligned) take
+//     2-byte register loads and 2-byte LDS writes instead, into the same layout (padding cleared once).
+// Epilogue: DPP shift-add of the three accumulator sets, the K halves summed through LDS, bias + ReLU + one RNE
+// rounding (the reference's apply_epilogue order, src/kernels/fused_epilogue.cuh:11-16) into a [filter][pixel]
+// tile in LDS, then contiguous NCHW runs per filter (8-byte stores when aligned). split > 1: FP32 partials
+// partial[z][NCHW] over the z-th range of channel slices [floor(S*z/split), floor(S*(z+1)/split)), the partition of
+// src/kernels/tensor_core_mma.cu:112-115, reduced by splitk_reduce.hip.
+// Grid: units (split, image, slab, 32-filter block), filter block fastest; XCD x (slot mod 8) takes a contiguous
+// range of units, so each XCD's L2 holds few images and every filter block.
+#include <algorithm>
+
+#include "lds_pipe.h"
+
+namespace gie_hip {
+namespace {
+
+constexpr int kSlTO = 32;  // output channels per workgroup
+
+struct SlabGeom {
+  int B, C, H, W, O, HW;
+  int S;                       // channel slices
+  int n_bands, n_ob, n_units;  // slabs per image, 32-filter blocks, workgroup units
+  int per_xcd;                 // units per XCD
+  int x_bytes, w_bytes;
+  int relu, split;
+  int y_vec;                   // outputs leave as 4-byte pixel pairs
+  long long total;             // |Y| elements (partial stride)
+  float inv_hw, inv_w;         // 1 / HW, 1 / W for fdiv
+};
+
+template <int P, int NBW, int NST>
+struct SlabShape {
+  static constexpr int G = P >= 16 ? 16 : P;            // spacing of the pixel-fragment reads (positions)
+  static constexpr int RW = 16 * NBW / P;               // output rows per wave
+  static constexpr int RB = 2 * RW;                     // output rows per slab
+  static constexpr int NR = RB + 2;                     // LDS rows per channel (halo row above and below)
+  static constexpr int NBR = (16 * (NBW - 1) + 2 * P) / G + 1;  // pixel-fragment reads per slice
+  static constexpr int CS = 32;                         // channels per slice (one MFMA k-step)
+  static constexpr int NW = 4, NT = 256;                // waves: (filter half) x (row half), one per SIMD
+  // weights: per filter the slice's OIHW run (CS * 9 halves) in 16-byte chunks + one pad chunk
+  static constexpr int WCH = CS * 18 / 16;
+  static constexpr int CPF = WCH + 1;
+  static constexpr int WPITCH = CPF * 16;
+  static constexpr int WBLK = (kSlTO * CPF + 63) / 64;  // 1 KiB load blocks holding data per slice
+  static constexpr int KBW = (WBLK + NW - 1) / NW;      // weight blocks per wave: every wave issues the same
+  static constexpr int WST = KBW * NW * 1024;           // count, the blocks past WBLK load zeros
+  // activations: per channel NS segments of 16 positions (32 bytes)
+  static constexpr int NS = ((NR * P + 15) / 16 + 7) / 8 * 8;
+  static constexpr int CHP = NS * 32;
+  static constexpr int ACT = CS * CHP;
+  static constexpr int R = CHP / 256;                   // 4-byte load instructions per channel
+  static constexpr int KA = ACT / 256 / NW;             // 4-byte load instructions per wave per slice
+  static constexpr int KR = (CS * NR * (P - 1) + NT - 1) / NT;  // 2-byte form: elements per thread per slice
+  static constexpr int KX = (CS * RB * (P - 1) / 8 + NT - 1) / NT;  // 16-byte form: chunks per thread per slice
+  static constexpr int LDS = NST * (ACT + WST);         // [activation stages][weight stages]
+  static constexpr int U = NST % 2 == 0 ? NST : 2 * NST;  // loop unroll: stage and register set are constants
+  static_assert((16 * NBW) % P == 0, "a wave's rows are whole 16-position blocks");
+  static_assert(KA == 8 * R, "each wave's load instructions cover 8 whole channels");
+  static_assert(CHP % 256 == 0, "channel regions start on the same bank");
+  static_assert((NST - 1) * ACT < 65536 && (NST - 1) * WST + 256 < 65536, "stage offsets fit the LDS offset field");
+  static_assert(LDS <= kLdsLimit, "LDS budget");
+};
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) u32x4 lds_v4;
+typedef __attribute__((address_space(3))) uint16_t lds_h;
+__device__ __forceinline__ u32x4 rd16(unsigned a) { return *reinterpret_cast<const lds_v4*>(size_t(a)); }
+__device__ __forceinline__ u32x2 rd_tr(unsigned a) {
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4s*>(size_t(a)));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// 4 bytes per lane straight into LDS at lds_base + 4 * lane (buffer_load_dword ... lds)
+__device__ __forceinline__ void dma4(v4i rsrc, unsigned lds_base, int voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(
+                   __builtin_amdgcn_readfirstlane(lds_base)),
+               "v"(voff), "s"(rsrc)
+               : "m0");
+}
+
+// segment slot swizzle of a channel: the 8 channels one half-wave reads (4 consecutive, and the 4 eight higher)
+// land on 8 distinct 32-byte bank groups
+__device__ __forceinline__ int seg_swz(int ch) { return (ch & 3) | (((ch >> 3) & 1) << 2); }
+
+// half a of the 144-byte weight run (8 channels x 9 taps) in the low 16 bits, half b in the high 16 bits
+__device__ __forceinline__ uint32_t pick2(const uint32_t (&d)[36], int a, int b) {
+  const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;          // bytes of S1 = d[a >> 1]
+  const uint32_t hi = (b & 1) ? 0x07060000u : 0x05040000u;  // bytes of S0 = d[b >> 1]
+  return __builtin_amdgcn_perm(d[b >> 1], d[a >> 1], lo | hi);
+}
+
+// lane i of each 16-lane row takes lane i + k (row_shl) or i - k (row_shr); lanes without a source read 0
+template <int CTRL>
+__device__ __forceinline__ f32x4 dpp4(const f32x4& v) {
+  f32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), CTRL, 0xf, 0xf, true));
+  return r;
+}
+constexpr int kShl1 = 0x101, kShl15 = 0x10F, kShr1 = 0x111, kShr15 = 0x11F;
+
+// direct-to-LDS loads whose per-slice advance travels in the scalar offset, so the per-lane offsets are set up once
+// (the resource is wave-uniform by construction; readfirstlane states it for the compiler)
+__device__ __forceinline__ v4i uniform4(v4i r) {
+  return v4i{__builtin_amdgcn_readfirstlane(r.x), __builtin_amdgcn_readfirstlane(r.y),
+             __builtin_amdgcn_readfirstlane(r.z), __builtin_amdgcn_readfirstlane(r.w)};
+}
+__device__ __forceinline__ void dma4s(v4i rsrc, unsigned lds_base, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(
+                   __builtin_amdgcn_readfirstlane(lds_base)),
+               "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "m0");
+}
+__device__ __forceinline__ void dma16s(v4i rsrc, unsigned lds_base, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(
+                   __builtin_amdgcn_readfirstlane(lds_base)),
+               "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "m0");
+}
+
+// register loads the compiler does not see as loads: valid after a counted wait_vmcnt (then touch_v)
+__device__ __forceinline__ u32x4 load16s(v4i rsrc, int voff, int soff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
+               : "=v"(v)
+               : "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff)));
+  return v;
+}
+__device__ __forceinline__ uint32_t load2s(v4i rsrc, int voff, int soff) {
+  uint32_t v;
+  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen"
+               : "=v"(v)
+               : "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff)));
+  return v;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n < 64 known only at run time (prologue bookkeeping)
+template <int N>
+__device__ __forceinline__ void wait_vm_upto(int n) {
+  if constexpr (N > 0) {
+    if (n >= N) {
+      wait_vm<N>();
+      return;
+    }
+    wait_vm_upto<N - 1>(n);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+// Activation load forms: kX16 = the whole image's 32-channel block by 16-byte register loads, written as pixel pairs;
+// kDma4 = 4-byte direct-to-LDS loads of every padded position; kReg2 = 2-byte register loads (odd rows).
+constexpr int kX16 = 0, kDma4 = 1, kReg2 = 2;
+
+template <typename E, int P, int NBW, int NST, int MODE>
+__global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                     float* __restrict__ partial, SlabGeom g) {
+  using Sh = SlabShape<P, NBW, NST>;
+  constexpr int CS = Sh::CS, NW = Sh::NW, NT = Sh::NT, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G;
+  constexpr int NBR = Sh::NBR, CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW;
+  constexpr int WST = Sh::WST, CHP = Sh::CHP, ACT = Sh::ACT, KA = Sh::KA, R = Sh::R, U = Sh::U;
+  constexpr int KX = Sh::KX, KR = Sh::KR;
+  constexpr bool REG = MODE != kDma4;                   // activations through registers
+  constexpr int NL = MODE == kX16 ? KX : (MODE == kReg2 ? KR : 0);  // register loads per thread per slice
+  constexpr int NI = KBW + (MODE == kDma4 ? KA : NL);   // loads per wave per slice
+  constexpr int WOFF = NST * ACT;                       // LDS: [activation stages][weight stages]
+  static_assert(NST * NI < 64, "loads in flight fit the vmcnt counter");
+  static_assert(!REG || NST >= 3, "register forms write a slice one step after loading it");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fh = wave & 1, wr = wave >> 1;
+
+  // ---- unit: XCD (slot mod 8) takes units [xcd * per_xcd, ...), filter block fastest ----
+  const int slot = int(blockIdx.x);
+  const int unit = (slot >> 3) + (slot & 7) * g.per_xcd;
+  if (unit >= g.n_units) return;  // workgroup-uniform
+  int rest = unit;
+  const int ob = rest % g.n_ob;
+  rest /= g.n_ob;
+  const int band = rest % g.n_bands;
+  rest /= g.n_bands;
+  const int b = rest % g.B, z = rest / g.B;
+  const int o0 = ob * kSlTO, oh0 = band * RB;
+  const int s_beg = (g.S * z) / g.split, ns = (g.S * (z + 1)) / g.split - s_beg;
+  const int nrows = min(RB, g.H - oh0);
+
+  const v4i xr = make_vsharp(x, g.x_bytes);
+  const v4i wrs = make_vsharp(w, g.w_bytes);
+  const unsigned lds0 = lds_addr(lds);
+
+  // bias bits of the lane's four filters, fetched now, used in the epilogue
+  const int f0 = o0 + fh * 16 + 4 * (lane >> 4);  // the lane's first filter
+  uint32_t bbits[4] = {0u, 0u, 0u, 0u};
+  if (g.split == 1 && bias != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bbits[i] = bias[min(f0 + i, g.O - 1)];
+  }
+
+  // ---- weight loads: block wave + NW * kb; lane slot u = (filter u / CPF, chunk u % CPF); per slice += CS * 18
+  int w_voff[KBW];
+#pragma unroll
+  for (int kb = 0; kb < KBW; ++kb) {
+    const int u = (wave + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
+    w_voff[kb] = (f < kSlTO && k < WCH && o0 + f < g.O) ? (o0 + f) * g.C * 18 + 16 * k : kOut;
+  }
+  int w_soff = s_beg * CS * 18;  // scalar offset of the next slice to load
+  int w_rem = g.C - s_beg * CS;  // its channels still inside C
+  int a_c0 = s_beg * CS;         // first channel of the next slice to load (activations)
+
+  // ---- activations, direct form: instruction i of this wave covers 256 bytes of channel 8 * wave + i / R;
+  // the per-lane offsets depend on (i % R, the channel's swizzle) only ----
+  constexpr int NV = MODE == kDma4 ? 4 * R : 1;
+  int a_voff[NV];
+  const int a_soff0 = (b * g.C + 8 * wave) * g.HW * 2;  // + (slice channel + i / R) * HW * 2
+  if constexpr (MODE == kDma4) {
+    const int swz_hi = (wave & 1) << 2;  // channel bit 3 = wave & 1 for all of this wave's channels
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int seg = (v % R) * 8 + (lane >> 3);
+      const int pos = ((seg ^ ((v / R) | swz_hi)) << 4) + 2 * (lane & 7);
+      const int row = pos / P, col = pos % P, ih = oh0 - 1 + row;
+      a_voff[v] = (row < NR && ih >= 0 && ih < g.H && col < g.W) ? (ih * g.W + col) * 2 : kOut;
+    }
+  }
+  // ---- activations, register forms: the thread's elements of the slice (fixed across slices) ----
+  // kX16: chunk c = k * NT + tid = halves 8c .. 8c+7 of the image's contiguous 32-channel block, as 4 pixel pairs
+  // kReg2: element e = k * NT + tid of (channel, input row of the slab, column)
+  int r_voff[NL > 0 ? NL : 1];
+  unsigned r_dst[NL > 0 ? NL : 1][MODE == kX16 ? 4 : 1];
+  int r_lim[NL > 0 ? NL : 1];  // element index (kX16: half index of the pair) compared against the slice's channels
+  u32x4 r_v16[MODE == kX16 ? NL : 1];
+  uint32_t r_v2[MODE == kReg2 ? NL : 1];
+  const int blk = CS * g.HW;  // halves of the block (kX16)
+  if constexpr (MODE == kX16) {
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int c = k * NT + tid;
+      r_voff[k] = 8 * c < blk ? 16 * c : kOut;
+      r_lim[k] = 8 * c;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = min(8 * c + 2 * q, blk - 2);
+        const int ch = fdiv(e, g.HW, g.inv_hw), px = e - ch * g.HW;
+        const int row = fdiv(px, g.W, g.inv_w), col = px - row * g.W;
+        const int pos = (row + 1) * P + col;
+        r_dst[k][q] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
+      }
+    }
+  } else if constexpr (MODE == kReg2) {
+    const int ih_lo = max(oh0 - 1, 0), ih_hi = min(oh0 + RB + 1, g.H);
+    const int per_ch = (ih_hi - ih_lo) * g.W;
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int e = k * NT + tid, ch = e / per_ch, rem = e - ch * per_ch, rr = rem / g.W, col = rem - rr * g.W;
+      const int pos = (ih_lo - oh0 + 1 + rr) * P + col;
+      r_voff[k] = ch < CS ? (ch * g.HW + (ih_lo + rr) * g.W + col) * 2 : kOut;
+      r_lim[k] = ch < CS ? ch : (1 << 24);
+      r_dst[k][0] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
+    }
+  }
+
+  // the next slice in order: activations (register forms: into registers v16 / v2, written one step later)...
+  auto issue_act = [&](int st, u32x4 (&v16)[MODE == kX16 ? NL : 1], uint32_t (&v2)[MODE == kReg2 ? NL : 1])
+                       __attribute__((always_inline)) {
+    if constexpr (MODE == kDma4) {
+      const unsigned ab = lds0 + unsigned(st * ACT + wave * KA * 256);
+#pragma unroll
+      for (int i = 0; i < KA; ++i) {
+        const int soff = a_soff0 + (a_c0 + i / R) * g.HW * 2;
+        dma4s(xr, ab + unsigned(i * 256), a_c0 + 8 * wave + i / R < g.C ? a_voff[(i % R) + R * ((i / R) & 3)] : kOut,
+              soff);
+      }
+    } else if constexpr (MODE == kX16) {
+      const int soff = (b * g.C + a_c0) * g.HW * 2;
+#pragma unroll
+      for (int k = 0; k < NL; ++k) v16[k] = load16s(xr, r_voff[k], soff);
+    } else {
+      const int soff = (b * g.C + a_c0) * g.HW * 2;
+#pragma unroll
+      for (int k = 0; k < NL; ++k) v2[k] = load2s(xr, a_c0 + r_lim[k] < g.C ? r_voff[k] : kOut, soff);
+    }
+    a_c0 += CS;
+  };
+  // ...then its weights
+  auto issue_w = [&](int st) __attribute__((always_inline)) {
+    const unsigned wb = lds0 + unsigned(WOFF + st * WST);
+    if (w_rem >= CS) {
+#pragma unroll
+      for (int kb = 0; kb < KBW; ++kb) dma16s(wrs, wb + unsigned((wave + NW * kb) * 1024), w_voff[kb], w_soff);
+    } else {  // the slice runs past C: chunks holding channels >= C load zeros
+#pragma unroll
+      for (int kb = 0; kb < KBW; ++kb) {
+        const int u = (wave + NW * kb) * 64 + lane, k = u - (u / CPF) * CPF;
+        dma16s(wrs, wb + unsigned((wave + NW * kb) * 1024), 8 * k < 9 * w_rem ? w_voff[kb] : kOut, w_soff);
+      }
+    }
+    w_soff += CS * 18;
+    w_rem -= CS;
+  };
+  // register forms: activations loaded into registers (set v) by an earlier issue, for the slice with channel base
+  // c0, written into stage st (the caller has waited for them)
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
+  auto write_regs = [&](int st, int c0, const u32x4 (&v16)[MODE == kX16 ? NL : 1],
+                        const uint32_t (&v2)[MODE == kReg2 ? NL : 1]) __attribute__((always_inline)) {
+    if constexpr (MODE == kX16) {
+      const int lim = (g.C - c0) * g.HW;  // halves of the block inside C
+      if (lim >= blk) {
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+          // chunk slots wholly inside the block write unconditionally; the others only where the chunk exists
+          if ((k + 1) * NT * 8 <= blk || r_voff[k] != kOut) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) *reinterpret_cast<lds_u32*>(size_t(r_dst[k][q] + unsigned(st * ACT))) = v16[k][q];
+          }
+        }
+      } else {  // the slice runs past C: pairs of channels >= C are written as zeros
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+          if (r_voff[k] != kOut) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<lds_u32*>(size_t(r_dst[k][q] + unsigned(st * ACT))) = r_lim[k] + 2 * q < lim ? v16[k][q] : 0u;
+          }
+        }
+      }
+    } else if constexpr (MODE == kReg2) {
+#pragma unroll
+      for (int k = 0; k < NL; ++k)
+        if (r_lim[k] < CS) *reinterpret_cast<lds_h*>(size_t(r_dst[k][0] + unsigned(st * ACT))) = uint16_t(v2[k]);
+    }
+  };
+  auto touch_regs = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      if constexpr (MODE == kX16) touch_v(r_v16[k]);
+      if constexpr (MODE == kReg2) touch_v(r_v2[k]);
+    }
+  };
+
+  // ---- fragment addresses (stage 0; the stage offset is the instruction's immediate offset) ----
+  // A: lane (filter fh*16 + lane%16, channels 8*(lane/16) .. +7): 144 contiguous bytes of the staging row
+  const unsigned a_rd = lds0 + unsigned(WOFF + (fh * 16 + (lane & 15)) * WPITCH + 8 * (lane >> 4) * 18);
+  // B: block u (16 positions from wr*RW*P + u*G), channel quads h = 0, 1 of the lane's k-group; each lane reads the
+  // 4 positions 4*(lane%4) .. +3 of channel row (lane%16)/4 of the quad
+  unsigned b_rd[NBR][2];
+#pragma unroll
+  for (int u = 0; u < NBR; ++u) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ch = 8 * (lane >> 4) + 4 * h + ((lane & 15) >> 2);
+      const int pos = wr * RW * P + u * G + 4 * (lane & 3);
+      b_rd[u][h] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
+    }
+  }
+
+  f32x4 acc[3][NBW];
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[s][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // two fragment sets: slice i multiplies from set i & 1 while slice i + 1 is read into the other
+  u32x4 fw[2][9], fb[2][NBR];
+  uint32_t d[36];
+  auto read_b = [&](int st, int set, int u0, int u1) __attribute__((always_inline)) {  // blocks u0 .. u1-1
+#pragma unroll
+    for (int u = u0; u < u1; ++u) {
+      const u32x2 lo = rd_tr(b_rd[u][0] + unsigned(st * ACT)), hi = rd_tr(b_rd[u][1] + unsigned(st * ACT));
+      fb[set][u] = u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
+  };
+  auto read_a = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const u32x4 v = rd16(a_rd + unsigned(st * WST + 16 * t));
+      d[4 * t] = v.x, d[4 * t + 1] = v.y, d[4 * t + 2] = v.z, d[4 * t + 3] = v.w;
+    }
+  };
+  auto transpose_a = [&](int set, int t0, int t1) __attribute__((always_inline)) {  // taps t0 .. t1-1
+#pragma unroll
+    for (int t = t0; t < t1; ++t)
+      fw[set][t] = u32x4{pick2(d, t, 9 + t), pick2(d, 18 + t, 27 + t), pick2(d, 36 + t, 45 + t), pick2(d, 54 + t, 63 + t)};
+  };
+  auto mfma_tap = [&](int set, int t) __attribute__((always_inline)) {  // the NBW MFMAs of tap t = (r, s)
+    const int r = t / 3, sc = t % 3;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[sc][j] = E::mfma(fw[set][t], fb[set][(16 * j + r * P) / G], acc[sc][j]);
+  };
+
+  // ---- prologue: slices 0 .. NST-1 loading (one per stage); register forms write slices 0 .. NST-2 now, from
+  // loads all issued before the first wait ----
+  if constexpr (REG) {
+    // padding positions are never written, so every activation stage starts zeroed
+    for (int i = tid * 16; i < NST * ACT; i += NT * 16) *reinterpret_cast<u32x4*>(lds + i) = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
+  {
+    u32x4 p16[NST - 1][MODE == kX16 ? NL : 1];
+    uint32_t p2[NST - 1][MODE == kReg2 ? NL : 1];
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      if (st < ns) {
+        if (st + 1 < NST) issue_act(st, p16[st], p2[st]);
+        else issue_act(st, r_v16, r_v2);  // written in step 0
+        issue_w(st);
+      }
+    }
+    if constexpr (REG) {
+      // slice st's activations are followed by its weights and everything of the slices after it
+#pragma unroll
+      for (int st = 0; st + 1 < NST; ++st) {
+        if (st < ns) {
+          // issued after slice st's activations: its weights and the slices st+1 .. min(NST, ns)-1
+          wait_vm_upto<KBW + (NST - 1) * Sh::KX + (NST - 1) * KBW + 8>(KBW + (min(NST, ns) - 1 - st) * NI);
+#pragma unroll
+          for (int k = 0; k < NL; ++k) {
+            if constexpr (MODE == kX16) touch_v(p16[st][k]);
+            if constexpr (MODE == kReg2) touch_v(p2[st][k]);
+          }
+          write_regs(st, (s_beg + st) * CS, p16[st], p2[st]);
+        }
+      }
+    }
+  }
+  // slice 0 has landed (register forms: written); slices 1 .. NST-1 may still be in flight
+  if (NST <= ns) wait_vmcnt<(NST - 1) * NI>();
+  else wait_vmcnt<0>();
+  stage_barrier();
+  if (ns > 0) {
+    read_b(0, 0, 0, NBR);
+    read_a(0);
+    transpose_a(0, 0, 9);
+  }
+
+  // ---- step i: slice i multiplies (9 tap groups of NBW MFMAs) while, between the groups, slice i + NST - 1's
+  // activations (register forms, loaded in step i - 1) are written, slice i + NST starts loading into slice i's
+  // stage (its fragments were read in step i - 1, which every wave finished before this step's barrier), and
+  // slice i + 1's fragments are read and transposed ----
+  auto step = [&](int i, auto u_c) __attribute__((always_inline)) {
+    constexpr int uu = decltype(u_c)::value;
+    constexpr int cur = uu & 1, nxt = cur ^ 1;
+    constexpr int st_next = (uu + 1) % NST;         // stage holding slice i + 1
+    constexpr int st_load = uu % NST;               // stage of slice i, reloaded with slice i + NST
+    constexpr int st_write = (uu + NST - 1) % NST;  // stage of slice i + NST - 1 (register forms)
+    const bool more = i + 1 < ns;
+    const bool wr_now = REG && i + NST - 1 < ns && more;
+    const bool ld_now = i + NST < ns;
+    if (more) {
+      // slice i + 1 has landed for every wave (this wave's loads counted: slices i+2 .. i+NST-1 may be in flight;
+      // the barrier covers the other waves)
+      if constexpr (NST > 2) {
+        if (i + NST - 1 < ns) wait_vmcnt<(NST - 2) * NI>();
+        else wait_vmcnt<0>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      stage_barrier();
+    }
+    // register forms: slice i + NST - 1's activations (issued last step, before its weights) have landed
+    if (wr_now) {
+      wait_vm<KBW>();
+      touch_regs();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // The LDS counter waits in issue order (and counts at most 15), so the weight fragments of slice i + 1 are
+    // requested first and transposed before any other LDS access is issued; the activation writes and the pixel
+    // fragments follow (the latter are consumed only in the next step).
+    mfma_tap(cur, 0);
+    if (more) read_a(st_next);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 2);
+    if (more) transpose_a(nxt, 0, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 3);
+    if (more) transpose_a(nxt, 3, 6);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 4);
+    if (more) transpose_a(nxt, 6, 9);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 5);
+    if (wr_now) write_regs(st_write, (s_beg + i + NST - 1) * CS, r_v16, r_v2);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 6);
+    if (ld_now) {
+      issue_act(st_load, r_v16, r_v2);
+      issue_w(st_load);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 7);
+    if (more) read_b(st_next, nxt, 0, (NBR + 1) / 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tap(cur, 8);
+    if (more) read_b(st_next, nxt, (NBR + 1) / 2, NBR);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int i = 0; i < ns; i += U) {
+    step(i, std::integral_constant<int, 0>{});
+    if (i + 1 < ns) step(i + 1, std::integral_constant<int, 1 % U>{});
+    if constexpr (U > 2) {
+      if (i + 2 < ns) step(i + 2, std::integral_constant<int, 2 % U>{});
+      if (i + 3 < ns) step(i + 3, std::integral_constant<int, 3 % U>{});
+    }
+    if constexpr (U > 4) {
+      if (i + 4 < ns) step(i + 4, std::integral_constant<int, 4 % U>{});
+      if (i + 5 < ns) step(i + 5, std::integral_constant<int, 5 % U>{});
+    }
+  }
+
+  // ---- epilogue: tap-column shifts, bias + ReLU + one rounding, stores straight from the registers ----
+  float bv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bv[i] = E::to_f32(uint16_t(bbits[i]));
+  const uint32_t oddm = 0u - uint32_t(lane & 1);  // all ones on odd lanes
+  const bool all_f = o0 + kSlTO <= g.O;            // the whole 32-filter block exists (wave-uniform)
+  const long long fbase = (static_cast<long long>(b) * g.O + f0) * g.HW;
+  // pixel-pair stores: even lane (column c) stores filters 0, 1 at (c, c+1), odd lane filters 2, 3 at (c-1, c)
+  uint16_t* const ypair = y + fbase + (static_cast<long long>(g.HW * 2 - 1) & (long long)(int)oddm);
+  float* const pdst = partial + static_cast<long long>(z) * g.total + fbase;
+  const int f_pair = f0 + int(oddm & 2u);
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
+    if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
+    if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
+    const int p = wr * RW * P + 16 * j + (lane & 15);
+    const int row = p / P, col = p % P;
+    const int pix = (oh0 + row) * g.W + col;
+    const bool valid = col < g.W && row < nrows;
+    if (g.split > 1) {
+      if (valid) {
+        if (all_f) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pdst[pix + i * g.HW] = out[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (f0 + i < g.O) pdst[pix + i * g.HW] = out[i];
+        }
+      }
+      continue;
+    }
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = out[i] + bv[i];
+      if (g.relu) v = fmaxf(v, 0.0f);
+      h[i] = E::from_f32(v);
+    }
+    if (g.y_vec) {
+      const uint32_t lo01 = h[0] | (h[1] << 16), lo23 = h[2] | (h[3] << 16);
+      const uint32_t send = (lo01 & oddm) | (lo23 & ~oddm);
+      const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap lane pairs
+      // even: (h0, recv.lo) and (h1, recv.hi); odd: (recv.lo, h2) and (recv.hi, h3)
+      const uint32_t wa_e = (h[0] & 0xffffu) | (recv << 16), wb_e = (h[1] & 0xffffu) | (recv & 0xffff0000u);
+      const uint32_t wa_o = (recv & 0xffffu) | (h[2] << 16), wb_o = (recv >> 16) | (h[3] << 16);
+      const uint32_t wa = (wa_o & oddm) | (wa_e & ~oddm), wb = (wb_o & oddm) | (wb_e & ~oddm);
+      // the odd lane's pair starts at column c - 1, which is valid when its own column is
+      if (col - int(oddm & 1u) < g.W && row < nrows) {
+        uint32_t* const da = reinterpret_cast<uint32_t*>(ypair + pix);
+        if (all_f || f_pair < g.O) da[0] = wa;
+        if (all_f || f_pair + 1 < g.O) da[g.HW / 2] = wb;
+      }
+    } else if (valid) {
+      uint16_t* const dst = y + fbase + pix;
+      if (all_f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i * g.HW] = uint16_t(h[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (f0 + i < g.O) dst[i * g.HW] = uint16_t(h[i]);
+      }
+    }
+  }
+}
+
+struct SlabCfg {
+  int P, NBW, NST;
+};
+// (row pitch, 16-position blocks per wave, load stages)
+constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3}, {16, 7, 2}, {16, 4, 3}, {8, 2, 3}, {8, 4, 3}, {32, 4, 3}};
+constexpr int kSlabN = int(sizeof(kSlabCfgs) / sizeof(kSlabCfgs[0]));
+
+template <int I>
+struct CfgT {
+  static constexpr int P = kSlabCfgs[I].P, NBW = kSlabCfgs[I].NBW, NST = kSlabCfgs[I].NST;
+  using Sh = SlabShape<P, NBW, NST>;
+};
+
+typedef void (*SlabFn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, SlabGeom);
+
+// the 2-byte register form exists where it needs at most 16 loads per thread and slice
+// (the register forms write a slice one step after loading it, so they need three stages or more)
+template <int I>
+SlabFn pick_fn(bool bf, int mode) {
+  using C = CfgT<I>;
+  if (mode == kDma4)
+    return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kDma4> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kDma4>;
+  if constexpr (C::NST >= 3) {
+    if (mode == kX16)
+      return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kX16> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kX16>;
+    if constexpr (C::Sh::KR <= 16)
+      return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kReg2> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kReg2>;
+  }
+  return nullptr;
+}
+
+struct SlabShapeInfo {
+  int P, RB, CS, NT, LDS;
+};
+
+template <int I>
+SlabShapeInfo shape_of() {
+  using Sh = typename CfgT<I>::Sh;
+  return SlabShapeInfo{CfgT<I>::P, Sh::RB, Sh::CS, Sh::NT, Sh::LDS};
+}
+
+template <int... Is>
+bool dispatch(int cfg, bool bf, int mode, SlabFn* fn, SlabShapeInfo* si, std::integer_sequence<int, Is...>) {
+  bool hit = false;
+  ((cfg == Is ? (*si = shape_of<Is>(), *fn = pick_fn<Is>(bf, mode), hit = true) : false), ...);
+  return hit;
+}
+
+struct SlabPlan {
+  SlabGeom g;
+  SlabFn fn;
+  int nt, lds;
+};
+
+// Geometry checks and launch parameters of configuration cfg; the activation load form and the output store width
+// are decided from the pointers.
+int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, const void* y, const float* partial,
+                 int split, SlabPlan* sp) {
+  if (cfg < 0 || cfg >= kSlabN || !gg) return GIE_HIP_EINVAL;
+  if (gg->kernel_h != 3 || gg->kernel_w != 3 || gg->stride_h != 1 || gg->stride_w != 1 || gg->pad_h != 1 ||
+      gg->pad_w != 1)
+    return GIE_HIP_EUNSUPPORTED;
+  if (gg->batch <= 0 || gg->in_channels <= 0 || gg->out_channels <= 0 || gg->in_h <= 0 || gg->in_w <= 0)
+    return GIE_HIP_EINVAL;
+  if (gg->in_channels % 8 != 0) return GIE_HIP_EUNSUPPORTED;  // 16-byte chunks of the weight runs
+  const long long hw = 1LL * gg->in_h * gg->in_w;
+  const bool bf = dtype == GIE_HIP_BF16;
+  SlabShapeInfo si{};
+  SlabFn fn = nullptr;
+  if (!dispatch(cfg, bf, kDma4, &fn, &si, std::make_integer_sequence<int, kSlabN>{})) return GIE_HIP_EINVAL;
+  if (gg->in_w + 1 > si.P) return GIE_HIP_EUNSUPPORTED;
+  const int bands = (gg->in_h + si.RB - 1) / si.RB;
+  // activation load form: even rows take 4-byte loads (16-byte register loads when the slab is the whole image and
+  // x is 16-byte aligned); odd rows or a 2-byte aligned x take 2-byte loads
+  const bool even = gg->in_w % 2 == 0 && !(reinterpret_cast<uintptr_t>(x) & 3u);
+  SlabFn alt = nullptr;
+  if (even && bands == 1 && !(reinterpret_cast<uintptr_t>(x) & 15u)) {
+    dispatch(cfg, bf, kX16, &alt, &si, std::make_integer_sequence<int, kSlabN>{});
+    if (alt != nullptr) fn = alt;  // configurations without the register forms keep the direct loads
+  }
+  if (!even) {
+    dispatch(cfg, bf, kReg2, &alt, &si, std::make_integer_sequence<int, kSlabN>{});
+    fn = alt;
+  }
+  if (fn == nullptr) return GIE_HIP_EUNSUPPORTED;
+  const long long xb = 2LL * gg->batch * gg->in_channels * hw;
+  const long long wb = 18LL * gg->out_channels * gg->in_channels;
+  const long long total = 1LL * gg->batch * gg->out_channels * hw;
+  if (xb >= (1LL << 30) || wb >= (1LL << 30) || total >= (1LL << 31)) return GIE_HIP_EUNSUPPORTED;
+  const int S = (gg->in_channels + si.CS - 1) / si.CS;
+  if (split < 1 || split > S) return GIE_HIP_EINVAL;
+  SlabGeom& g = sp->g;
+  g.B = gg->batch, g.C = gg->in_channels, g.H = gg->in_h, g.W = gg->in_w, g.O = gg->out_channels, g.HW = int(hw);
+  g.S = S;
+  g.n_bands = bands;
+  g.n_ob = (g.O + kSlTO - 1) / kSlTO;
+  const long long units = 1LL * split * g.B * bands * g.n_ob;
+  if (units > (1LL << 30)) return GIE_HIP_EUNSUPPORTED;
+  g.n_units = int(units);
+  g.per_xcd = (g.n_units + 7) / 8;
+  g.x_bytes = int(xb), g.w_bytes = int(wb);
+  g.relu = gg->relu;
+  g.split = split;
+  g.total = total;
+  g.inv_hw = 1.0f / float(hw);
+  g.inv_w = 1.0f / float(gg->in_w);
+  // 4-byte stores of pixel pairs: even rows, so every pair starts on an even element of a 4-byte aligned y
+  g.y_vec = split == 1 && gg->in_w % 2 == 0 && !(reinterpret_cast<uintptr_t>(y) & 3u);
+  sp->fn = fn;
+  sp->nt = si.NT;
+  sp->lds = si.LDS;
+  return GIE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace gie_hip
+
+using namespace gie_hip;
+
+extern "C" int gie_hip_slab_config_count(void) { return kSlabN; }
+
+extern "C" int gie_hip_slab_config_get(int index, gie_slab_config* out) {
+  if (index < 0 || index >= kSlabN || !out) return GIE_HIP_EINVAL;
+  gie_conv_geom g{};
+  g.batch = 1, g.in_channels = 64, g.in_h = 2, g.in_w = 2, g.out_channels = 1;  // even rows: either load form
+  g.kernel_h = g.kernel_w = 3, g.stride_h = g.stride_w = 1, g.pad_h = g.pad_w = 1;
+  SlabPlan sp;
+  if (int rc = slab_prepare(index, &g, GIE_HIP_FP16, nullptr, nullptr, nullptr, 1, &sp)) return rc;
+  const SlabCfg& c = kSlabCfgs[index];
+  out->tile_m = kSlTO;
+  out->rows = 2 * (16 * c.NBW / c.P);
+  out->pitch = c.P;
+  out->tile_k = 32;
+  out->stages = c.NST;
+  out->threads = sp.nt;
+  out->lds_bytes = sp.lds;
+  out->version = 3;
+  return GIE_HIP_OK;
+}
+
+extern "C" int gie_hip_slab_check(int config, const gie_conv_geom* g, int* lds_bytes) {
+  SlabPlan sp;
+  if (int rc = slab_prepare(config, g, GIE_HIP_FP16, nullptr, nullptr, nullptr, 1, &sp)) return rc;
+  if (lds_bytes) *lds_bytes = sp.lds;
+  return GIE_HIP_OK;
+}
+
+extern "C" int gie_hip_conv_slab(int config, int dtype, const gie_conv_geom* gg, const void* x, const void* w,
+                                 const void* bias, void* y, float* partial, int split, void* stream) {
+  if (!gg || !x || !w) return GIE_HIP_EINVAL;
+  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
+  if (split > 1 ? partial == nullptr : y == nullptr) return GIE_HIP_EINVAL;
+  if ((bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) || (y && (reinterpret_cast<uintptr_t>(y) & 1u)) ||
+      (reinterpret_cast<uintptr_t>(x) & 1u) || (partial && (reinterpret_cast<uintptr_t>(partial) & 3u)))
+    return GIE_HIP_EINVAL;
+  if (reinterpret_cast<uintptr_t>(w) & 15u) return GIE_HIP_EUNSUPPORTED;  // 16-byte weight chunks
+  SlabPlan sp;
+  if (int rc = slab_prepare(config, gg, dtype, x, y, partial, split, &sp)) return rc;
+  if (int rc = set_lds_limit(reinterpret_cast<const void*>(sp.fn), sp.lds)) return rc;
+  hipLaunchKernelGGL(sp.fn, dim3(unsigned(8 * sp.g.per_xcd)), dim3(unsigned(sp.nt)), sp.lds,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
+                     static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+                     partial, sp.g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GIE_HIP_OK : int(e);
+}

@@ -14,6 +14,7 @@ void register_pw_family(std::vector<KernelDesc>& out);    // pw_family.cpp
 void register_f32_family(std::vector<KernelDesc>& out);   // f32_family.cpp
 void register_stem_family(std::vector<KernelDesc>& out);  // stem_family.cpp
 void register_narrow_family(std::vector<KernelDesc>& out);  // narrow_family.cpp
+void register_slab_family(std::vector<KernelDesc>& out);    // slab_family.cpp
 
 std::string KernelDesc::describe() const {
   std::ostringstream os;
@@ -35,6 +36,7 @@ std::vector<KernelDesc>& registry_storage() {
     register_f32_family(r);
     register_stem_family(r);  // after mfma: its unaligned-pointer fallback is an mfma entry
     register_narrow_family(r);  // likewise
+    register_slab_family(r);    // likewise
     std::set<std::string> names;
     for (const auto& k : r) {
       if (!names.insert(k.name).second) throw Error(StatusCode::kInternal, "duplicate kernel name " + k.name);

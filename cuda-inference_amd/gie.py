@@ -73,6 +73,11 @@ class GieBandConfig(ctypes.Structure):
                                             "stages", "version")]
 
 
+class GieSlabConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "rows", "pitch", "tile_k", "stages", "threads", "lds_bytes",
+                                            "version")]
+
+
 class GieIgemmConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "tile_m", "tile_n", "tile_k", "waves_m", "waves_n", "threads", "lds_bytes", "stages", "version")]
@@ -186,6 +191,10 @@ _HIP = {
     "gie_hip_conv_stem": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_narrow_check": ([_GP, _vp], _i),
     "gie_hip_conv_narrow": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
+    "gie_hip_slab_config_count": ([], _i),
+    "gie_hip_slab_config_get": ([_i, ctypes.POINTER(GieSlabConfig)], _i),
+    "gie_hip_slab_check": ([_i, _GP, _ip], _i),
+    "gie_hip_conv_slab": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_f32_config_count": ([], _i),
     "gie_hip_f32_config_tile_m": ([_i], _i),
     "gie_hip_f32_check": ([_i, _GP, _vp], _i),

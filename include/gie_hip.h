@@ -26,6 +26,10 @@
  *   gie_hip_conv_stem, _stem_check   transposes + tcmma_kernel for the 7x7 stride-2 stem (in_channels <= 4), fused
  *   gie_hip_conv_narrow, _narrow_check transposes + tcmma_kernel (+ split-K reduce) for 3x3 layers with few pixels
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,309-316
+ *   gie_hip_conv_slab, _slab_check   both transposes + tcmma_kernel (split-K partials included) for 3x3 stride-1
+ *                                    layers, fused: one launch straight from NCHW x / OIHW w
+ *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,297-324
+ *   gie_hip_slab_config_*            the registered tile table             src/kernels/tensor_core_mma.cu:370-388
  *   gie_hip_conv_f32, _f32_check     implicit_gemm_kernel<<<>>> launch (FP32) and the TF32 path
  *                                                                         src/kernels/implicit_gemm.cu:47-189,204-214
  *   gie_hip_f32_config_*             the registered FP32 tile table        src/kernels/implicit_gemm.cu:218-268
@@ -210,6 +214,31 @@ int gie_hip_conv_stem(int dtype, const gie_conv_geom* g, const void* x, const vo
 int gie_hip_narrow_check(const gie_conv_geom* g, int* lds_bytes);
 int gie_hip_conv_narrow(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
                         void* stream);
+
+/* One registered slab configuration: tile_m (32) output channels x a slab of `rows` output rows of one image laid
+   out `pitch` positions per row (in_w + 1 <= pitch), channel slices of tile_k, `stages` LDS load stages. */
+typedef struct gie_slab_config {
+  int tile_m, rows, pitch, tile_k;
+  int stages;
+  int threads;
+  int lds_bytes;
+  int version;
+} gie_slab_config;
+
+int gie_hip_slab_config_count(void);
+int gie_hip_slab_config_get(int index, gie_slab_config* out);
+/* 0 when configuration `config` runs geometry g (3x3 filter, stride 1, padding 1, in_channels % 4 == 0,
+   in_w + 1 <= pitch, sizes within 32-bit offsets), with the LDS bytes per workgroup in *lds_bytes. */
+int gie_hip_slab_check(int config, const gie_conv_geom* g, int* lds_bytes);
+
+/* Slab convolution on MFMA 16x16x32 (FP32 accumulation) straight from the caller's NCHW x (any 2-byte alignment;
+   8-byte loads when x is 8-byte aligned and every slab's input run starts on a 4-pixel boundary) and OIHW w
+   (8-byte aligned, GIE_HIP_EUNSUPPORTED otherwise): no repack, no workspace. split == 1: y (NCHW, any 2-byte
+   alignment) = round(relu?(acc + bias)), one rounding. split > 1: partial[z][NCHW index] = FP32 sum over the
+   channel slices [floor(S*z/split), floor(S*(z+1)/split)), S = ceil(in_channels / tile_k); reduce with
+   gie_hip_splitk_reduce. 1 <= split <= S. */
+int gie_hip_conv_slab(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w,
+                      const void* bias, void* y, float* partial, int split, void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
    dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */

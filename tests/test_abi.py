@@ -160,3 +160,47 @@ def test_narrow_geometry_check_on_host():
         assert 0 < lds.value <= 160 * 1024
     p = gie.Problem(2, 1024, 56, 56, 64, 3, 3, 1, 1, 1, 1, precision="fp16")
     assert gie.hip().gie_hip_narrow_check(ctypes.byref(p.geom(1024)), None) != 0
+
+
+def test_slab_configuration_table_on_host():
+    """Every slab configuration answers its table query (the registry builds its entries from it) with a
+    consistent shape, and the slab registry entries exist for both precisions and every split factor."""
+    h = gie.hip()
+    n = h.gie_hip_slab_config_count()
+    assert n >= 4
+    for i in range(n):
+        c = gie.GieSlabConfig()
+        assert h.gie_hip_slab_config_get(i, ctypes.byref(c)) == 0, i
+        assert c.tile_m == 32 and c.tile_k == 32 and c.pitch in (8, 16, 32) and 2 <= c.stages <= 4
+        assert c.threads == 256
+        assert (c.rows // 2) * c.pitch % 16 == 0
+        assert 0 < c.lds_bytes <= 160 * 1024
+    assert h.gie_hip_slab_config_get(n, ctypes.byref(gie.GieSlabConfig())) != 0
+    names = gie.registry()
+    for prec in ("fp16", "bf16"):
+        for sk in (1, 2, 4, 8):
+            assert any(k.startswith(f"slab_{prec}_3x3_") and k.endswith(f"_sk{sk}") for k in names), (prec, sk)
+
+
+def test_slab_geometry_check_on_host():
+    """gie_hip_slab_check is host arithmetic: the GPU slab tests' shapes qualify for some configuration, and the
+    geometries the kernel cannot run are refused by all."""
+    h = gie.hip()
+    n = h.gie_hip_slab_config_count()
+    for B, C, H, W, K in [(2, 64, 14, 14, 32), (3, 128, 14, 14, 40), (2, 72, 13, 10, 20), (2, 72, 13, 7, 20),
+                          (1, 64, 29, 14, 32), (2, 64, 7, 6, 32), (8, 512, 7, 7, 64), (2, 64, 28, 28, 48),
+                          (1, 32, 5, 3, 8), (2, 8, 6, 6, 5), (32, 256, 14, 14, 256), (8, 512, 7, 7, 512)]:
+        p = gie.Problem(B, C, H, W, K, 3, 3, 1, 1, 1, 1, precision="fp16")
+        ok = 0
+        for i in range(n):
+            lds = ctypes.c_int(0)
+            if h.gie_hip_slab_check(i, ctypes.byref(p.geom(C)), ctypes.byref(lds)) == 0:
+                assert 0 < lds.value <= 160 * 1024
+                ok += 1
+        assert ok > 0, (B, C, H, W, K)
+    for p in (gie.Problem(2, 64, 7, 7, 64, 5, 5, 1, 1, 2, 2, precision="fp16"),
+              gie.Problem(2, 64, 7, 7, 64, 3, 3, 2, 2, 1, 1, precision="fp16"),
+              gie.Problem(2, 132, 7, 7, 64, 3, 3, 1, 1, 1, 1, precision="fp16"),
+              gie.Problem(1, 64, 8, 40, 32, 3, 3, 1, 1, 1, 1, precision="fp16")):
+        for i in range(n):
+            assert h.gie_hip_slab_check(i, ctypes.byref(p.geom(p.in_channels)), None) != 0
