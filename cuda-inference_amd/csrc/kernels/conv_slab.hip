@@ -36,6 +36,8 @@
 // Grid: units (split, image, slab, 32-filter block), filter block fastest; XCD x (slot mod 8) takes a contiguous
 // range of units, so each XCD's L2 holds few images and every filter block.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "lds_pipe.h"
 
@@ -721,6 +723,79 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   return GIE_HIP_OK;
 }
 
+int launch_slab(const SlabPlan& sp, const void* x, const void* w, const void* bias, void* y, float* partial,
+                void* stream) {
+  hipLaunchKernelGGL(sp.fn, dim3(unsigned(8 * sp.g.per_xcd)), dim3(unsigned(sp.nt)), sp.lds,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
+                     static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+                     partial, sp.g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GIE_HIP_OK : int(e);
+}
+
+// Pointer checks shared by the entry points: x, y, bias 2-byte aligned, partials 4-byte aligned; w must be 16-byte
+// aligned for the 16-byte weight chunks (GIE_HIP_EUNSUPPORTED otherwise, so a caller can fall back).
+int check_pointers(int dtype, const void* x, const void* w, const void* bias, const void* y, const float* partial) {
+  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
+  if ((bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) || (y && (reinterpret_cast<uintptr_t>(y) & 1u)) ||
+      (reinterpret_cast<uintptr_t>(x) & 1u) || (partial && (reinterpret_cast<uintptr_t>(partial) & 3u)))
+    return GIE_HIP_EINVAL;
+  if (reinterpret_cast<uintptr_t>(w) & 15u) return GIE_HIP_EUNSUPPORTED;
+  return GIE_HIP_OK;
+}
+
+// ---- allocation-free variant ---------------------------------------------------------------------------------------
+// gie_hip_conv_slab_noalloc keeps its FP32 split-K partials in `scratch`, a file-scope device array: every GPU the
+// library runs on holds its own copy (kSlabScratchFloats floats = 32 MiB) from module load until the process ends.
+// Host code never passes `scratch` itself (on the host that name is a stand-in, not a device address): the first
+// call on a device looks up that device's address with hipGetSymbolAddress and every later call uses the kept one.
+constexpr long long kSlabScratchFloats = 8LL << 20;
+static __device__ __align__(256) float scratch[kSlabScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int raise_lds_limits() {
+  for (int cfg = 0; cfg < kSlabN; ++cfg)
+    for (int bf = 0; bf < 2; ++bf)
+      for (int mode : {kX16, kDma4, kReg2}) {
+        SlabFn fn = nullptr;
+        SlabShapeInfo si{};
+        if (!dispatch(cfg, bf != 0, mode, &fn, &si, std::make_integer_sequence<int, kSlabN>{}) || fn == nullptr ||
+            si.LDS <= 64 * 1024)
+          continue;
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, si.LDS);
+        if (e != hipSuccess) return int(e);
+      }
+  return GIE_HIP_OK;
+}
+
+// Device address of the current device's `scratch`. Set-up, once per device with that device current: the symbol
+// lookup and the LDS opt-in of every slab kernel (so no later call allocates host bookkeeping either).
+int scratch_of_current_device(float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return int(hipErrorInvalidDevice);
+  if (dev < 0 || dev >= kMaxDevices) return GIE_HIP_EUNSUPPORTED;
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return int(e);
+      if (addr == nullptr) return int(hipErrorInvalidSymbol);
+      if (int rc = raise_lds_limits()) return rc;
+      p = static_cast<float*>(addr);
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return GIE_HIP_OK;
+}
+
 }  // namespace
 }  // namespace gie_hip
 
@@ -757,19 +832,27 @@ extern "C" int gie_hip_slab_check(int config, const gie_conv_geom* g, int* lds_b
 extern "C" int gie_hip_conv_slab(int config, int dtype, const gie_conv_geom* gg, const void* x, const void* w,
                                  const void* bias, void* y, float* partial, int split, void* stream) {
   if (!gg || !x || !w) return GIE_HIP_EINVAL;
-  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
   if (split > 1 ? partial == nullptr : y == nullptr) return GIE_HIP_EINVAL;
-  if ((bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) || (y && (reinterpret_cast<uintptr_t>(y) & 1u)) ||
-      (reinterpret_cast<uintptr_t>(x) & 1u) || (partial && (reinterpret_cast<uintptr_t>(partial) & 3u)))
-    return GIE_HIP_EINVAL;
-  if (reinterpret_cast<uintptr_t>(w) & 15u) return GIE_HIP_EUNSUPPORTED;  // 16-byte weight chunks
+  if (int rc = check_pointers(dtype, x, w, bias, y, partial)) return rc;
   SlabPlan sp;
   if (int rc = slab_prepare(config, gg, dtype, x, y, partial, split, &sp)) return rc;
   if (int rc = set_lds_limit(reinterpret_cast<const void*>(sp.fn), sp.lds)) return rc;
-  hipLaunchKernelGGL(sp.fn, dim3(unsigned(8 * sp.g.per_xcd)), dim3(unsigned(sp.nt)), sp.lds,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
-                     static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
-                     partial, sp.g);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? GIE_HIP_OK : int(e);
+  return launch_slab(sp, x, w, bias, y, partial, stream);
 }
+
+extern "C" int gie_hip_conv_slab_noalloc(int config, int dtype, const gie_conv_geom* gg, const void* x, const void* w,
+                                         const void* bias, void* y, int split, void* stream) {
+  if (!gg || !x || !w || !y) return GIE_HIP_EINVAL;
+  if (int rc = check_pointers(dtype, x, w, bias, y, nullptr)) return rc;
+  float* part = nullptr;
+  if (int rc = scratch_of_current_device(&part)) return rc;
+  SlabPlan sp;
+  if (int rc = slab_prepare(config, gg, dtype, x, y, split > 1 ? part : nullptr, split, &sp)) return rc;
+  if (split > 1 && 1LL * split * sp.g.total > kSlabScratchFloats) return GIE_HIP_ESCRATCH;
+  // every unit of range z writes its whole share of partial[z], so the scratch needs no clearing between calls
+  if (int rc = launch_slab(sp, x, w, bias, y, split > 1 ? part : nullptr, stream)) return rc;
+  if (split == 1) return GIE_HIP_OK;
+  return gie_hip_splitk_reduce(dtype, part, bias, y, sp.g.total, split, sp.g.O, sp.g.HW, sp.g.relu, stream);
+}
+
+extern "C" long long gie_hip_slab_scratch_floats(void) { return kSlabScratchFloats; }

@@ -295,5 +295,6 @@ extern "C" const char* gie_hip_status_string(int status) {
   if (status == GIE_HIP_OK) return "ok";
   if (status == GIE_HIP_EINVAL) return "invalid argument";
   if (status == GIE_HIP_EUNSUPPORTED) return "unsupported by this kernel configuration";
+  if (status == GIE_HIP_ESCRATCH) return "request exceeds the library's static scratch";
   return hipGetErrorString(static_cast<hipError_t>(status));
 }

@@ -195,6 +195,8 @@ _HIP = {
     "gie_hip_slab_config_get": ([_i, ctypes.POINTER(GieSlabConfig)], _i),
     "gie_hip_slab_check": ([_i, _GP, _ip], _i),
     "gie_hip_conv_slab": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
+    "gie_hip_conv_slab_noalloc": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _i, _vp], _i),
+    "gie_hip_slab_scratch_floats": ([], ctypes.c_longlong),
     "gie_hip_f32_config_count": ([], _i),
     "gie_hip_f32_config_tile_m": ([_i], _i),
     "gie_hip_f32_check": ([_i, _GP, _vp], _i),

@@ -51,6 +51,7 @@ extern "C" {
 #define GIE_HIP_OK 0
 #define GIE_HIP_EINVAL (-1)      /* null pointer, bad size, shape the kernel's grid cannot cover */
 #define GIE_HIP_EUNSUPPORTED (-2) /* valid request this kernel configuration cannot run */
+#define GIE_HIP_ESCRATCH (-3)     /* request needs more than the library's static scratch */
 
 /* element types; numbering follows gie::Precision (kFp32 = 0, kFp16 = 1, kBf16 = 2, kTf32 = 3). TF32 is FP32
    storage whose multiplier inputs are rounded to TF32 inside the kernel. */
@@ -227,18 +228,30 @@ typedef struct gie_slab_config {
 
 int gie_hip_slab_config_count(void);
 int gie_hip_slab_config_get(int index, gie_slab_config* out);
-/* 0 when configuration `config` runs geometry g (3x3 filter, stride 1, padding 1, in_channels % 4 == 0,
+/* 0 when configuration `config` runs geometry g (3x3 filter, stride 1, padding 1, in_channels % 8 == 0,
    in_w + 1 <= pitch, sizes within 32-bit offsets), with the LDS bytes per workgroup in *lds_bytes. */
 int gie_hip_slab_check(int config, const gie_conv_geom* g, int* lds_bytes);
 
-/* Slab convolution on MFMA 16x16x32 (FP32 accumulation) straight from the caller's NCHW x (any 2-byte alignment;
-   8-byte loads when x is 8-byte aligned and every slab's input run starts on a 4-pixel boundary) and OIHW w
-   (8-byte aligned, GIE_HIP_EUNSUPPORTED otherwise): no repack, no workspace. split == 1: y (NCHW, any 2-byte
-   alignment) = round(relu?(acc + bias)), one rounding. split > 1: partial[z][NCHW index] = FP32 sum over the
-   channel slices [floor(S*z/split), floor(S*(z+1)/split)), S = ceil(in_channels / tile_k); reduce with
-   gie_hip_splitk_reduce. 1 <= split <= S. */
+/* Slab convolution on MFMA 16x16x32 (FP32 accumulation) straight from the caller's NCHW x and OIHW w: no repack,
+   no workspace at split 1. x: any 2-byte alignment (16-byte register loads when the slab is the whole image and x
+   is 16-byte aligned, 4-byte direct-to-LDS loads for even rows on a 4-byte aligned x, 2-byte loads otherwise;
+   GIE_HIP_EUNSUPPORTED when the configuration lacks the form needed). w: 16-byte aligned, GIE_HIP_EUNSUPPORTED
+   otherwise. split == 1: y (NCHW, any 2-byte alignment) = round(relu?(acc + bias)), one rounding. split > 1:
+   partial[z][NCHW index] = FP32 sum over the channel slices [floor(S*z/split), floor(S*(z+1)/split)),
+   S = ceil(in_channels / tile_k); reduce with gie_hip_splitk_reduce. 1 <= split <= S. */
 int gie_hip_conv_slab(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w,
                       const void* bias, void* y, float* partial, int split, void* stream);
+
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+   tight serving loops, harnesses that forbid hipMalloc): gie_hip_conv_slab followed, for split > 1, by
+   gie_hip_splitk_reduce, with the FP32 partials in the library's static per-device scratch of
+   gie_hip_slab_scratch_floats() floats (32 MiB) instead of a caller buffer. Allocates nothing; the first call on a
+   device sets that device up. split * batch * out_channels * in_h * in_w above the scratch size: GIE_HIP_ESCRATCH.
+   Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU (other streams, other threads)
+   race. */
+int gie_hip_conv_slab_noalloc(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w,
+                              const void* bias, void* y, int split, void* stream);
+long long gie_hip_slab_scratch_floats(void);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
    dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */
