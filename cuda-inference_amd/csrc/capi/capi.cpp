@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -114,6 +115,41 @@ const KernelDesc& kernel_named(const char* name) {
   const KernelDesc* k = find_kernel(name);
   GIE_REQUIRE(k != nullptr, StatusCode::kInvalidArgument, std::string("unknown kernel '") + name + "'");
   return *k;
+}
+
+DeviceInfo modelled_device(const gie_device_model& d) {
+  GIE_REQUIRE(d.cus > 0 && d.mfma_tflops > 0 && d.fp32_tflops > 0 && d.hbm_gbs > 0 && d.launch_us >= 0,
+              StatusCode::kInvalidArgument, "device model needs positive CU count and ceilings");
+  DeviceInfo dev;
+  dev.device = -1;
+  dev.name = "modelled gfx950 device";
+  dev.gcn_arch = "gfx950:sramecc+:xnack-";
+  dev.cc_major = 9;
+  dev.cc_minor = 5;
+  dev.sm_count = d.cus;
+  dev.global_mem_bytes = size_t(288) << 30;
+  dev.l2_bytes = size_t(4) << 20;
+  dev.smem_per_block_default = 64 * 1024;
+  dev.smem_per_block_optin = d.lds_per_workgroup;
+  dev.smem_per_sm = 160 * 1024;
+  dev.regs_per_sm = 4 * 512 * 64;
+  dev.max_threads_per_sm = 2048;
+  dev.max_threads_per_block = 1024;
+  dev.max_blocks_per_sm = 32;
+  dev.warp_size = 64;
+  dev.max_sm_clock_khz = 2400000;
+  return dev;
+}
+
+DeviceCeilings modelled_ceilings(const gie_device_model& d) {
+  DeviceCeilings c;
+  c.fp16_tc_tflops = d.mfma_tflops;
+  c.fp32_tflops = d.fp32_tflops;
+  c.bw_gbs = d.hbm_gbs;
+  c.launch_overhead_us = d.launch_us;
+  c.measured = false;
+  c.source = "caller-described device";
+  return c;
 }
 
 HipGraphExecutor::Enqueue chain_enqueue(int n, void* const* plans, const void* const* xs, const void* const* ws,
@@ -412,6 +448,40 @@ int gie_estimate_kernel(const char* name, const gie_problem* p, double* out6, in
     const double v[6] = {e.time_us, e.compute_us, e.memory_us, e.launch_us, e.tile_efficiency, e.wave_efficiency};
     std::memcpy(out6, v, sizeof(v));
     if (bound) *bound = int(e.bound);
+  });
+}
+
+int gie_model_estimate(const char* name, const gie_problem* p, const gie_device_model* d, double* out6, int* bound) {
+  return guarded([&] {
+    GIE_REQUIRE(d != nullptr && out6 != nullptr, StatusCode::kInvalidArgument, "null device model or output");
+    const DeviceInfo dev = modelled_device(*d);
+    const Estimate e = estimate_kernel(to_problem(p), kernel_named(name), dev, modelled_ceilings(*d));
+    const double v[6] = {e.time_us, e.compute_us, e.memory_us, e.launch_us, e.tile_efficiency, e.wave_efficiency};
+    std::memcpy(out6, v, sizeof(v));
+    if (bound) *bound = int(e.bound);
+  });
+}
+
+int gie_model_rank(const gie_problem* p, const gie_device_model* d, char* buf, size_t n, double* us, int max,
+                   int* count) {
+  return guarded([&] {
+    GIE_REQUIRE(d != nullptr, StatusCode::kInvalidArgument, "null device model");
+    const ConvProblem pr = to_problem(p);
+    validate_problem(pr);
+    const DeviceInfo dev = modelled_device(*d);
+    const DeviceCeilings c = modelled_ceilings(*d);
+    std::vector<std::pair<std::string, double>> order;
+    for (const KernelDesc* k : Dispatcher::compatible_kernels(pr, dev))
+      order.emplace_back(k->name, estimate_kernel(pr, *k, dev, c).time_us);
+    std::stable_sort(order.begin(), order.end(), [](const auto& a, const auto& b) { return a.second < b.second; });
+    std::string names;
+    for (size_t i = 0; i < order.size(); ++i) {
+      if (int(i) < max && us) us[i] = order[i].second;
+      if (i) names += "\n";
+      names += order[i].first;
+    }
+    copy_str(names, buf, n);
+    if (count) *count = int(order.size());
   });
 }
 

@@ -107,6 +107,22 @@ struct Fns {
     if (gie_hip_band_check(e().config, &g, &bytes) != GIE_HIP_OK) return 0;
     return size_t(bytes);
   }
+  // Useful output positions of a workgroup's tile_n-position band (rows of a power-of-two padded width, one image
+  // per band), times the filter and channel padding.
+  static double tile_efficiency(const ConvProblem& prob) {
+    const Entry& en = e();
+    const Conv2DParams& p = prob.p;
+    int owp = 1;
+    while (owp < p.out_w()) owp *= 2;
+    const int rows = std::max(1, en.info.tile_n / owp);
+    const int64_t bands = (p.out_h() + rows - 1) / rows;
+    const double pos = double(p.out_h()) * p.out_w() / (double(bands) * en.info.tile_n);
+    const double o = double(p.out_channels) / double(((p.out_channels + en.info.tile_m - 1) / en.info.tile_m) *
+                                                     en.info.tile_m);
+    const double c = double(p.in_channels) / double(((p.in_channels + en.info.tile_k - 1) / en.info.tile_k) *
+                                                    en.info.tile_k);
+    return std::min(1.0, pos) * o * c;
+  }
   static int64_t blocks(const ConvProblem& prob) {
     // one workgroup per (32 output channels, image, band of rows); a band is tile_n / padded-row-width rows
     const Entry& en = e();
@@ -169,6 +185,7 @@ void fill_fns(int idx, KernelDesc& k) {
       k.num_blocks = &Fns<I>::blocks;
       k.extra_traffic_bytes = &Fns<I>::extra_traffic;
       k.blocks_per_cu = &Fns<I>::occupancy;
+      k.tile_efficiency = &Fns<I>::tile_efficiency;
       k.launch = &Fns<I>::launch;
       return;
     }
@@ -207,9 +224,7 @@ void register_band_family(std::vector<KernelDesc>& out) {
     k.tile_n = en.info.tile_n;
     k.tile_k = en.info.tile_k * en.info.kernel_h * en.info.kernel_w;
     k.uses_tensor_cores = true;
-    k.needs_lut = false;
     k.launches = 2 + (en.split > 1 ? 1 : 0);
-    k.efficiency_prior = 0.6;
     fill_fns<0>(int(i), k);
     out.push_back(std::move(k));
   }

@@ -1,16 +1,61 @@
-// Dispatcher (the reference's dispatcher.cpp:23-105 priority order): forced kernel > CPU reference is not
-// dispatchable > capability filter (throws with every rejection reason) > tuning-cache hit that is still
-// compatible > autotune on request > cost-model ranking.
+// Dispatcher: which registered kernel runs a problem (the behaviour of src/runtime/dispatcher.cpp:23-105).
+//
+// Selection is a fixed chain of rules, each of which either decides or passes to the next:
+//   1. a kernel named in the options (it must exist, belong to the forced backend if one is given, and support
+//      the problem; otherwise the call fails rather than silently running something else);
+//   2. the CPU reference is never a GPU choice;
+//   3. the capability filter leaves at least one candidate, or the call fails listing every rejected kernel with
+//      its reason, one "- name: reason" line each;
+//   4. a tuning-cache entry whose kernel is still among the candidates;
+//   5. a fresh autotune when the options ask for one;
+//   6. the best candidate under the cost model.
 #include "gpu_inference/dispatcher.h"
 
 #include <algorithm>
-#include <sstream>
+#include <string>
 
 #include "gpu_inference/autotuner.h"
 #include "gpu_inference/perf_model.h"
 #include "gpu_inference/roctx.h"
 
 namespace gie {
+namespace {
+
+Selection chosen(const KernelDesc* k, SelectionSource src, double us, const char* reason) {
+  Selection s;
+  s.kernel = k;
+  s.source = src;
+  s.predicted_us = us;
+  s.reason = reason;
+  return s;
+}
+
+Selection forced_kernel(const ConvProblem& prob, const DeviceInfo& dev, const Conv2DOptions& opt) {
+  const KernelDesc* k = find_kernel(opt.kernel);
+  if (k == nullptr) throw Error(StatusCode::kInvalidArgument, "no registered kernel is named '" + opt.kernel + "'");
+  if (opt.backend != Backend::kAuto && k->backend != opt.backend)
+    throw Error(StatusCode::kInvalidArgument, "kernel '" + opt.kernel + "' is a " + to_string(k->backend) +
+                                                  " kernel; the options force backend " + to_string(opt.backend));
+  std::string why;
+  if (!k->supports(prob, dev, &why)) throw Error(StatusCode::kUnsupported, k->name + " cannot run this problem: " + why);
+  return chosen(k, SelectionSource::kForcedKernel, 0.0, "kernel named in the options");
+}
+
+[[noreturn]] void nothing_runs(const ConvProblem& prob, const DeviceInfo& dev, Backend backend,
+                               const std::vector<Rejection>& rejected) {
+  std::string msg = "no " + std::string(backend == Backend::kAuto ? "" : to_string(backend)) +
+                    (backend == Backend::kAuto ? "" : " ") + "kernel runs " + prob.key() + " on " + dev.name + " (" +
+                    dev.gcn_arch + ")";
+  if (rejected.empty()) msg += ": the " + std::string(to_string(backend)) + " backend has no registered kernels";
+  for (const Rejection& r : rejected) msg += "\n  - " + r.kernel + ": " + r.reason;
+  throw Error(StatusCode::kUnsupported, msg);
+}
+
+bool contains(const std::vector<const KernelDesc*>& v, const KernelDesc* k) {
+  return std::find(v.begin(), v.end(), k) != v.end();
+}
+
+}  // namespace
 
 const char* to_string(SelectionSource s) {
   switch (s) {
@@ -25,70 +70,54 @@ const char* to_string(SelectionSource s) {
 
 std::vector<const KernelDesc*> Dispatcher::compatible_kernels(const ConvProblem& prob, const DeviceInfo& dev,
                                                               Backend only, std::vector<Rejection>* rejected) {
-  std::vector<const KernelDesc*> out;
+  std::vector<const KernelDesc*> accepted;
+  std::string why;
   for (const KernelDesc& k : kernel_registry()) {
     if (only != Backend::kAuto && k.backend != only) continue;
-    std::string why;
-    if (k.supports(prob, dev, &why)) out.push_back(&k);
-    else if (rejected) rejected->push_back({k.name, why});
+    why.clear();
+    if (k.supports(prob, dev, &why))
+      accepted.push_back(&k);
+    else if (rejected != nullptr)
+      rejected->push_back({k.name, why.empty() ? std::string("unsupported") : why});
   }
-  return out;
+  return accepted;
 }
 
 std::vector<std::pair<const KernelDesc*, double>> Dispatcher::rank_by_model(const ConvProblem& prob,
                                                                              const DeviceInfo& dev,
                                                                              const std::vector<const KernelDesc*>& cands) {
-  DeviceCeilings c;
-  if (!load_cached_ceilings(dev.device, &c)) c = theoretical_ceilings(dev);
-  std::vector<std::pair<const KernelDesc*, double>> ranked;
-  for (const KernelDesc* k : cands) ranked.emplace_back(k, estimate_kernel(prob, *k, dev, c).time_us);
-  std::stable_sort(ranked.begin(), ranked.end(), [](const auto& a, const auto& b) { return a.second < b.second; });
-  return ranked;
+  DeviceCeilings ceil;
+  if (!load_cached_ceilings(dev.device, &ceil)) ceil = theoretical_ceilings(dev);
+  std::vector<std::pair<const KernelDesc*, double>> order;
+  order.reserve(cands.size());
+  for (const KernelDesc* k : cands) order.emplace_back(k, estimate_kernel(prob, *k, dev, ceil).time_us);
+  // stable: equal estimates keep registry order, so the ranking is deterministic
+  std::stable_sort(order.begin(), order.end(),
+                   [](const std::pair<const KernelDesc*, double>& a, const std::pair<const KernelDesc*, double>& b) {
+                     return a.second < b.second;
+                   });
+  return order;
 }
 
 Selection Dispatcher::select(const ConvProblem& prob, const DeviceInfo& dev, const Conv2DOptions& opt) {
   RoctxRange range("gie::Dispatcher::select");
   validate_problem(prob);
-  Selection sel;
-
-  if (!opt.kernel.empty()) {
-    const KernelDesc* k = find_kernel(opt.kernel);
-    if (!k) throw Error(StatusCode::kInvalidArgument, "unknown kernel '" + opt.kernel + "'");
-    if (opt.backend != Backend::kAuto && k->backend != opt.backend)
-      throw Error(StatusCode::kInvalidArgument, "kernel '" + opt.kernel + "' belongs to backend " +
-                                                    to_string(k->backend) + ", not " + to_string(opt.backend));
-    std::string why;
-    if (!k->supports(prob, dev, &why)) throw Error(StatusCode::kUnsupported, k->name + ": " + why);
-    sel.kernel = k;
-    sel.source = SelectionSource::kForcedKernel;
-    sel.reason = "explicit kernel";
-    return sel;
-  }
+  if (!opt.kernel.empty()) return forced_kernel(prob, dev, opt);
   if (opt.backend == Backend::kCpuReference)
     throw Error(StatusCode::kUnsupported,
-                "the CPU reference runs on host buffers via cpu_conv2d_reference(); it is not a GPU backend");
+                "cpu_reference is a host routine (cpu_conv2d_reference on host buffers), not a GPU backend");
 
   std::vector<Rejection> rejected;
-  std::vector<const KernelDesc*> cands = compatible_kernels(prob, dev, opt.backend, &rejected);
-  if (cands.empty()) {
-    std::ostringstream os;
-    os << "no kernel can run " << prob.key() << " on " << dev.name << " (backend=" << to_string(opt.backend) << "):";
-    if (rejected.empty()) os << " no kernel is registered for this backend";
-    for (const auto& r : rejected) os << "\n  - " << r.kernel << ": " << r.reason;
-    throw Error(StatusCode::kUnsupported, os.str());
-  }
+  const std::vector<const KernelDesc*> cands = compatible_kernels(prob, dev, opt.backend, &rejected);
+  if (cands.empty()) nothing_runs(prob, dev, opt.backend, rejected);
 
-  TuneCache cache(opt.cache_path);
-  std::string cached_name;
-  double cached_us = 0;
-  if (!opt.force_retune && cache.lookup(prob, dev, &cached_name, &cached_us, nullptr, opt.backend)) {
-    const KernelDesc* k = find_kernel(cached_name);
-    if (k && std::find(cands.begin(), cands.end(), k) != cands.end()) {
-      sel.kernel = k;
-      sel.source = SelectionSource::kTuningCache;
-      sel.predicted_us = cached_us;
-      sel.reason = "measured winner from tuning cache";
-      return sel;
+  if (!opt.force_retune) {
+    std::string name;
+    double us = 0;
+    if (TuneCache(opt.cache_path).lookup(prob, dev, &name, &us, nullptr, opt.backend)) {
+      const KernelDesc* k = find_kernel(name);
+      if (k != nullptr && contains(cands, k))
+        return chosen(k, SelectionSource::kTuningCache, us, "fastest measured kernel, from the tuning cache");
     }
   }
   if (opt.autotune || opt.force_retune) {
@@ -96,19 +125,13 @@ Selection Dispatcher::select(const ConvProblem& prob, const DeviceInfo& dev, con
     to.only_backend = opt.backend;
     to.cache_path = opt.cache_path;
     to.force_retune = opt.force_retune;
-    TuneResult r = Autotuner::tune(prob, dev, to);
-    sel.kernel = find_kernel(r.best_kernel);
-    sel.source = SelectionSource::kTuned;
-    sel.predicted_us = r.best_us;
-    sel.reason = "autotuned";
-    return sel;
+    const TuneResult r = Autotuner::tune(prob, dev, to);
+    return chosen(find_kernel(r.best_kernel), SelectionSource::kTuned, r.best_us, "fastest measured kernel, tuned now");
   }
   const auto ranked = rank_by_model(prob, dev, cands);
-  sel.kernel = ranked.front().first;
-  sel.predicted_us = ranked.front().second;
-  sel.source = opt.backend == Backend::kAuto ? SelectionSource::kCostModel : SelectionSource::kForcedBackend;
-  sel.reason = "best-ranked by the analytical cost model (no measurement available)";
-  return sel;
+  return chosen(ranked.front().first,
+                opt.backend == Backend::kAuto ? SelectionSource::kCostModel : SelectionSource::kForcedBackend,
+                ranked.front().second, "lowest cost-model estimate (nothing measured for this problem)");
 }
 
 }  // namespace gie

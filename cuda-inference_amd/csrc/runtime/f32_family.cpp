@@ -114,9 +114,7 @@ KernelDesc make_entry() {
   k.tile_n = 128;
   k.tile_k = 16;
   k.uses_tensor_cores = false;  // priced against the FP32 ceiling, which the FP32 MFMA rate equals
-  k.needs_lut = false;
   k.launches = 1 + (Split > 1 ? 1 : 0);
-  k.efficiency_prior = 0.5;
   k.supports = &F::supports;
   k.workspace_bytes = &F::workspace;
   k.dynamic_smem_bytes = &F::lds;

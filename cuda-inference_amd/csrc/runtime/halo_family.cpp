@@ -203,9 +203,7 @@ void register_halo_family(std::vector<KernelDesc>& out) {
     k.tile_n = en.info.tile_n;
     k.tile_k = en.info.tile_k * en.info.kernel_h * en.info.kernel_w;
     k.uses_tensor_cores = true;
-    k.needs_lut = false;
     k.launches = 2 + (en.split > 1 ? 1 : 0);
-    k.efficiency_prior = 0.6;
     fill_fns<0>(int(i), k);
     out.push_back(std::move(k));
   }

@@ -1,4 +1,13 @@
-// hipGraph capture / update / replay of an enqueue function (the reference's cuda_graph.cpp on HIP graphs).
+// HipGraphExecutor (the role of src/runtime/cuda_graph.cpp:13-97): record a chain of asynchronous launches once as
+// a HIP graph and replay it with one hipGraphLaunch, which removes the per-launch host cost and the gaps between
+// small kernels.
+//
+// Recording happens on a private non-blocking stream in thread-local capture mode, so work other threads enqueue
+// meanwhile is neither captured nor made illegal. The enqueue function runs once eagerly before the first recording:
+// one-time work it may trigger (function attributes, lazy module loads) is not legal inside a capture. If the
+// enqueue function throws mid-recording, the capture is ended and its partial graph discarded before the exception
+// leaves. recapture_update() records again and first tries to patch the executable graph in place (same topology,
+// new kernel arguments such as buffer addresses); only when HIP refuses is the graph instantiated afresh.
 #include "gpu_inference/hip_graph.h"
 
 #include <hip/hip_runtime.h>
@@ -9,96 +18,106 @@
 
 namespace gie {
 namespace {
-using clock = std::chrono::steady_clock;
-double us_since(clock::time_point t0) { return std::chrono::duration<double, std::micro>(clock::now() - t0).count(); }
 
-struct StreamGuard {
-  hipStream_t s;
-  ~StreamGuard() { (void)hipStreamDestroy(s); }
+double micros_since(std::chrono::steady_clock::time_point t0) {
+  return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+}
+
+class PrivateStream {
+ public:
+  PrivateStream() { GIE_HIP_CHECK(hipStreamCreateWithFlags(&s_, hipStreamNonBlocking)); }
+  ~PrivateStream() { (void)hipStreamDestroy(s_); }
+  PrivateStream(const PrivateStream&) = delete;
+  PrivateStream& operator=(const PrivateStream&) = delete;
+  hipStream_t get() const { return s_; }
+
+ private:
+  hipStream_t s_ = nullptr;
 };
+
+// Records `enqueue` into a new graph; *us receives the recording time.
+hipGraph_t record(const HipGraphExecutor::Enqueue& enqueue, double* us) {
+  PrivateStream stream;
+  const auto t0 = std::chrono::steady_clock::now();
+  GIE_HIP_CHECK(hipStreamBeginCapture(stream.get(), hipStreamCaptureModeThreadLocal));
+  try {
+    enqueue(stream.get());
+  } catch (...) {
+    hipGraph_t partial = nullptr;
+    (void)hipStreamEndCapture(stream.get(), &partial);
+    if (partial != nullptr) (void)hipGraphDestroy(partial);
+    throw;
+  }
+  hipGraph_t g = nullptr;
+  GIE_HIP_CHECK(hipStreamEndCapture(stream.get(), &g));
+  *us = micros_since(t0);
+  return g;
+}
+
 }  // namespace
 
 HipGraphExecutor::~HipGraphExecutor() { reset(); }
 
 void HipGraphExecutor::reset() {
-  if (exec_) (void)hipGraphExecDestroy(exec_);
-  if (graph_) (void)hipGraphDestroy(graph_);
+  if (exec_ != nullptr) (void)hipGraphExecDestroy(exec_);
+  if (graph_ != nullptr) (void)hipGraphDestroy(graph_);
   exec_ = nullptr;
   graph_ = nullptr;
   nodes_ = 0;
 }
 
-void HipGraphExecutor::capture_graph(const Enqueue& enqueue, hipGraph_t* g, double* us) {
-  hipStream_t s;
-  GIE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-  StreamGuard guard{s};
-  const auto t0 = clock::now();
-  GIE_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-  try {
-    enqueue(s);
-  } catch (...) {
-    hipGraph_t partial = nullptr;
-    (void)hipStreamEndCapture(s, &partial);
-    if (partial) (void)hipGraphDestroy(partial);
-    throw;
-  }
-  GIE_HIP_CHECK(hipStreamEndCapture(s, g));
-  *us = us_since(t0);
+void HipGraphExecutor::adopt(hipGraph_t g, double capture_us) {
+  reset();
+  graph_ = g;
+  capture_us_ = capture_us;
+  const auto t0 = std::chrono::steady_clock::now();
+  GIE_HIP_CHECK(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
+  instantiate_us_ = micros_since(t0);
+  size_t n = 0;
+  GIE_HIP_CHECK(hipGraphGetNodes(graph_, nullptr, &n));
+  nodes_ = n;
 }
 
 void HipGraphExecutor::capture(const Enqueue& enqueue) {
   RoctxRange range("gie::HipGraphExecutor::capture");
-  reset();
   {
-    hipStream_t warm;
-    GIE_HIP_CHECK(hipStreamCreateWithFlags(&warm, hipStreamNonBlocking));
-    StreamGuard guard{warm};
-    enqueue(warm);
-    GIE_HIP_CHECK(hipStreamSynchronize(warm));
+    PrivateStream warm;
+    enqueue(warm.get());
+    GIE_HIP_CHECK(hipStreamSynchronize(warm.get()));
   }
-  capture_graph(enqueue, &graph_, &capture_us_);
-  const auto t0 = clock::now();
-  GIE_HIP_CHECK(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
-  instantiate_us_ = us_since(t0);
-  size_t n = 0;
-  GIE_HIP_CHECK(hipGraphGetNodes(graph_, nullptr, &n));
-  nodes_ = n;
+  double us = 0;
+  adopt(record(enqueue, &us), us);
 }
 
 bool HipGraphExecutor::recapture_update(const Enqueue& enqueue) {
-  if (!exec_) {
+  RoctxRange range("gie::HipGraphExecutor::recapture_update");
+  if (exec_ == nullptr) {
     capture(enqueue);
     return false;
   }
-  hipGraph_t g2 = nullptr;
   double us = 0;
-  capture_graph(enqueue, &g2, &us);
-  capture_us_ = us;
-  hipGraphNode_t err_node = nullptr;
-  hipGraphExecUpdateResult result = hipGraphExecUpdateError;
-  const hipError_t e = hipGraphExecUpdate(exec_, g2, &err_node, &result);
-  if (e == hipSuccess && result == hipGraphExecUpdateSuccess) {
+  hipGraph_t fresh = record(enqueue, &us);
+  hipGraphNode_t failed_node = nullptr;
+  hipGraphExecUpdateResult outcome = hipGraphExecUpdateError;
+  if (hipGraphExecUpdate(exec_, fresh, &failed_node, &outcome) == hipSuccess && outcome == hipGraphExecUpdateSuccess) {
     (void)hipGraphDestroy(graph_);
-    graph_ = g2;
+    graph_ = fresh;
+    capture_us_ = us;
     return true;
   }
-  (void)hipGetLastError();
-  (void)hipGraphExecDestroy(exec_);
-  exec_ = nullptr;
-  (void)hipGraphDestroy(graph_);
-  graph_ = g2;
-  const auto t0 = clock::now();
-  GIE_HIP_CHECK(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
-  instantiate_us_ = us_since(t0);
-  size_t n = 0;
-  GIE_HIP_CHECK(hipGraphGetNodes(graph_, nullptr, &n));
-  nodes_ = n;
+  (void)hipGetLastError();  // the refused update leaves an error code behind
+  try {
+    adopt(fresh, us);
+  } catch (...) {
+    if (graph_ != fresh) (void)hipGraphDestroy(fresh);
+    throw;
+  }
   return false;
 }
 
 void HipGraphExecutor::launch(hipStream_t stream) const {
   RoctxRange range("gie::HipGraphExecutor::launch");
-  GIE_REQUIRE(exec_ != nullptr, StatusCode::kInvalidArgument, "HipGraphExecutor::launch before capture()");
+  GIE_REQUIRE(exec_ != nullptr, StatusCode::kInvalidArgument, "HipGraphExecutor::launch called before capture()");
   GIE_HIP_CHECK(hipGraphLaunch(exec_, stream));
 }
 

@@ -219,9 +219,7 @@ void register_mfma_family(std::vector<KernelDesc>& out) {
     k.tile_n = en.info.tile_n;
     k.tile_k = en.info.tile_k;
     k.uses_tensor_cores = true;
-    k.needs_lut = false;  // the kernel walks (r, s, c) with an incremental cursor
     k.launches = 2 + (en.split > 1 ? 1 : 0);
-    k.efficiency_prior = 0.5;
     fill_fns<0>(int(i), k);
     out.push_back(std::move(k));
   }

@@ -105,9 +105,7 @@ KernelDesc make_entry() {
   k.tile_n = 32;
   k.tile_k = 16;
   k.uses_tensor_cores = true;
-  k.needs_lut = false;
   k.launches = 1;
-  k.efficiency_prior = 0.6;
   k.supports = &F::supports;
   k.workspace_bytes = &F::workspace;
   k.dynamic_smem_bytes = &F::lds;

@@ -1,6 +1,19 @@
-// Roofline cost model (the reference's perf_model.cpp structure: compulsory traffic, tile and wave efficiency,
-// per-family efficiency prior, launch overhead) + measured ceilings from the HIP microbenchmarks in
-// csrc/kernels/ceilings.hip (the reference's ceilings.cu role), cached per GPU as JSON.
+// Analytical cost model for MI355X (the role of src/runtime/perf_model.cpp:47-174) and the ceiling
+// microbenchmarks that calibrate it (csrc/kernels/ceilings.hip).
+//
+// Model of one forward call of kernel k on problem P:
+//   compute = FLOPs / (MFMA peak x family MFMA efficiency x tile efficiency x wave efficiency)
+//   memory  = (compulsory bytes + the kernel's extra traffic) / (HBM bandwidth x family HBM efficiency)
+//   fixed   = launches x dispatch cost + the family's cost of filling and draining a launch
+//   time    = max(compute, memory) + fixed      (reported as launch_us; "launch"-bound when it dominates)
+// * Family efficiencies are not guesses per backend: each is what that kernel family reached on an MI355X in the
+//   library's benchmark protocol (per-call time, inputs resident in HBM), listed in kFamilies with the measurement.
+// * Wave efficiency follows how gfx950 places workgroups: dispatch deals them round-robin to the 8 XCDs, and each
+//   XCD's 32 CUs hold blocks_per_cu of them at a time, so a launch runs in ceil(ceil(blocks / 8) / (32 x occ))
+//   waves and the last wave's empty slots are lost.
+// * The dispatch cost is the measured gap of back-to-back launches on one stream (measure_ceilings), 1.5 us
+//   before any measurement.
+// The model only orders candidates for problems nothing has been measured on; the autotuner decides by timing.
 #include "gpu_inference/perf_model.h"
 
 #include <hip/hip_runtime.h>
@@ -8,8 +21,11 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
+#include <filesystem>
 #include <map>
 #include <mutex>
+#include <system_error>
 
 #include "gie_hip.h"
 #include "gpu_inference/json_lite.h"
@@ -19,24 +35,61 @@
 namespace gie {
 namespace {
 
-std::mutex g_cal_mu;
-std::map<std::string, double>& cal_map() {
+constexpr double kDefaultDispatchUs = 1.5;
+constexpr int kXcds = 8;
+
+struct FamilyProfile {
+  const char* prefix;
+  double mfma_eff;  // steady-state fraction of the dense MFMA peak (the FP32 vector peak for f32_)
+  double hbm_eff;   // fraction of HBM bandwidth reached when bandwidth-bound
+  double fill_us;   // fixed cost of a launch: workgroup set-up, pipeline fill, epilogue drain of the last wave
+};
+
+// Fitted to per-call times of each family's best entry on one MI355X (256 CUs), inputs resident in HBM:
+//   L2 = 32x256x14x14 -> 256 3x3 fp16, L3 = 64x256x28x28 -> 1024 1x1 fp16, L4 = 64x3x224x224 -> 64 7x7/2 fp16,
+//   L5 = 8x512x7x7 -> 512 3x3 bf16.
+constexpr FamilyProfile kFamilies[] = {
+    {"slab_", 0.35, 0.45, 6.0},     // L2 17.2 us (431 TFLOP/s), L5 16.0 us at split 2; fill cost from in-kernel clocks
+    {"band_", 0.27, 0.45, 5.0},     // L2 18.9 us including the weight repack launch
+    {"halo_", 0.37, 0.40, 10.0},    // L2 23.3 us including the repack launch, L5 24.7 us at split 4
+    {"mfma_", 0.22, 0.35, 8.0},     // L2 25.7 us, L3 87 us, L4 145 us, L5 26.0 us at split 4
+    {"pws_", 0.30, 0.38, 2.0},      // L3 45.5 us = 2.84 TB/s of compulsory traffic
+    {"pw_", 0.30, 0.44, 2.0},       // L3 39.4 us = 3.27 TB/s
+    {"stem_", 0.25, 0.555, 2.0},     // L4 30.9 us = 3.95 TB/s
+    {"narrow_", 0.084, 0.30, 2.0},  // L5 15.0 us (123 TFLOP/s)
+    {"f32_", 0.30, 0.35, 2.0},      // FP32 / TF32 vector kernels: not benchmarked, assumed
+};
+
+const FamilyProfile* profile_of(const std::string& name) {
+  for (const FamilyProfile& f : kFamilies)
+    if (name.compare(0, std::strlen(f.prefix), f.prefix) == 0) return &f;
+  return nullptr;
+}
+
+std::mutex g_scale_mu;
+std::map<std::string, double>& backend_scale() {
   static std::map<std::string, double> m;
   return m;
 }
 
-double bytes_per_us(const DeviceCeilings& c) { return c.bw_gbs * 1e3; }
-double flops_per_us(double tflops) { return tflops * 1e6; }
-
-Bound classify(double compute_us, double memory_us, double launch_us) {
-  if (launch_us >= compute_us && launch_us >= memory_us) return Bound::kLaunch;
+Bound bound_of(double compute_us, double memory_us, double launch_us) {
+  if (launch_us >= std::max(compute_us, memory_us)) return Bound::kLaunch;
   return compute_us >= memory_us ? Bound::kCompute : Bound::kBandwidth;
 }
 
-std::string ceiling_path(int device) {
+// Fraction of the computed tile volume that is real work in the implicit-GEMM view.
+double padded_fraction(const ConvProblem& prob, const KernelDesc& k) {
+  const auto frac = [](int64_t v, int64_t tile) {
+    tile = std::max<int64_t>(tile, 1);
+    return double(v) / double(((v + tile - 1) / tile) * tile);
+  };
+  return frac(prob.p.gemm_m(), k.tile_m) * frac(prob.p.gemm_n(), k.tile_n) * frac(prob.p.gemm_k(), k.tile_k);
+}
+
+std::string ceiling_file(int device) {
   const DeviceInfo& d = DeviceInfo::get(device);
   std::string dir;
-  if (const char* p = std::getenv("GIE_CEILING_DIR")) dir = p;
+  if (const char* env = std::getenv("GIE_CEILING_DIR")) dir = env;
   else dir = std::string(std::getenv("HOME") ? std::getenv("HOME") : ".") + "/.cache/gpu_inference";
   std::string arch = d.gcn_arch;
   for (char& c : arch)
@@ -45,15 +98,38 @@ std::string ceiling_path(int device) {
          ".json";
 }
 
+class ScopedDevice {
+ public:
+  explicit ScopedDevice(int device) {
+    GIE_HIP_CHECK(hipGetDevice(&saved_));
+    GIE_HIP_CHECK(hipSetDevice(device));
+  }
+  ~ScopedDevice() { (void)hipSetDevice(saved_); }
+
+ private:
+  int saved_ = 0;
+};
+
+class ScopedStream {
+ public:
+  ScopedStream() { GIE_HIP_CHECK(hipStreamCreateWithFlags(&s_, hipStreamNonBlocking)); }
+  ~ScopedStream() { (void)hipStreamDestroy(s_); }
+  hipStream_t get() const { return s_; }
+
+ private:
+  hipStream_t s_ = nullptr;
+};
+
 }  // namespace
 
-void set_model_calibration(const std::map<std::string, double>& m) {
-  std::lock_guard<std::mutex> lock(g_cal_mu);
-  cal_map() = m;
+void set_model_calibration(const std::map<std::string, double>& scale_by_backend) {
+  std::lock_guard<std::mutex> lock(g_scale_mu);
+  backend_scale() = scale_by_backend;
 }
+
 std::map<std::string, double> get_model_calibration() {
-  std::lock_guard<std::mutex> lock(g_cal_mu);
-  return cal_map();
+  std::lock_guard<std::mutex> lock(g_scale_mu);
+  return backend_scale();
 }
 
 const char* to_string(Bound b) {
@@ -70,26 +146,30 @@ DeviceCeilings theoretical_ceilings(const DeviceInfo& dev) {
   c.fp32_tflops = dev.est_peak_fp32_tflops();
   c.fp16_tc_tflops = dev.est_peak_fp16_tc_tflops();
   c.bw_gbs = dev.est_peak_bw_gbs();
-  c.launch_overhead_us = 4.0;
+  c.launch_overhead_us = kDefaultDispatchUs;
   c.measured = false;
-  c.source = "theoretical estimate from CU count, max clock and CDNA throughput tables";
+  c.source = "spec estimate (CU count x clock x CDNA per-CU rates; HBM from the product table)";
   return c;
 }
 
 bool load_cached_ceilings(int device, DeviceCeilings* out) {
   try {
-    const json::Value v = json::parse_file(ceiling_path(device));
-    const json::Value* f = v.find("fp16_mfma_tflops");
-    const json::Value* b = v.find("bw_gbs");
-    const json::Value* l = v.find("launch_overhead_us");
-    if (!f || !b || !l) return false;
-    out->fp16_tc_tflops = f->as_double();
-    out->bw_gbs = b->as_double();
-    out->launch_overhead_us = l->as_double();
-    out->fp32_tflops = DeviceInfo::get(device).est_peak_fp32_tflops();
-    out->measured = true;
-    out->source = "measured (cached " + ceiling_path(device) + ")";
-    return out->fp16_tc_tflops > 0 && out->bw_gbs > 0;
+    const std::string path = ceiling_file(device);
+    const json::Value v = json::parse_file(path);
+    const json::Value* mfma = v.find("fp16_mfma_tflops");
+    const json::Value* bw = v.find("bw_gbs");
+    const json::Value* launch = v.find("launch_overhead_us");
+    if (mfma == nullptr || bw == nullptr || launch == nullptr) return false;
+    DeviceCeilings c;
+    c.fp16_tc_tflops = mfma->as_double();
+    c.bw_gbs = bw->as_double();
+    c.launch_overhead_us = launch->as_double();
+    c.fp32_tflops = DeviceInfo::get(device).est_peak_fp32_tflops();
+    c.measured = true;
+    c.source = "measured, cached in " + path;
+    if (c.fp16_tc_tflops <= 0 || c.bw_gbs <= 0) return false;
+    *out = c;
+    return true;
   } catch (const Error&) {
     return false;
   }
@@ -98,47 +178,41 @@ bool load_cached_ceilings(int device, DeviceCeilings* out) {
 DeviceCeilings measure_ceilings(int device, bool use_cache) {
   DeviceCeilings c;
   if (use_cache && load_cached_ceilings(device, &c)) return c;
-  int prev = 0;
-  GIE_HIP_CHECK(hipGetDevice(&prev));
-  GIE_HIP_CHECK(hipSetDevice(device));
-  struct Restore {
-    int d;
-    ~Restore() { (void)hipSetDevice(d); }
-  } restore{prev};
+  ScopedDevice scope(device);
   const DeviceInfo& dev = DeviceInfo::get(device);
   c = theoretical_ceilings(dev);
-  hipStream_t s;
-  GIE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-  struct SG {
-    hipStream_t s;
-    ~SG() { (void)hipStreamDestroy(s); }
-  } sg{s};
+  ScopedStream stream;
   TimingOptions to;
   to.warmup_iters = 3;
   to.samples = 10;
-  {  // matrix cores: 8 workgroups per CU, 4 independent MFMA chains per wave
-    DeviceBuffer sink(size_t(dev.sm_count) * 8 * 4);
+  {
+    // MFMA: 8 workgroups per CU, each wave running 4 independent 16x16x32 fp16 chains (16384 FLOP per MFMA)
     const int blocks = dev.sm_count * 8, iters = 2048;
+    DeviceBuffer sink(size_t(blocks) * 4);
     const TimingStats t = time_stream_work(
-        [&](hipStream_t st) {
-          check_kernel_status(gie_hip_ceiling_mfma(blocks, iters, static_cast<float*>(sink.data()), st), "mfma ceiling");
+        [&](hipStream_t s) {
+          check_kernel_status(gie_hip_ceiling_mfma(blocks, iters, static_cast<float*>(sink.data()), s),
+                              "MFMA ceiling");
         },
-        s, to);
-    const double flops = double(blocks) * 4.0 * iters * 4.0 * 16384.0;
-    c.fp16_tc_tflops = flops / (t.median_us * 1e6);
+        stream.get(), to);
+    c.fp16_tc_tflops = double(blocks) * 4.0 * iters * 4.0 * 16384.0 / (t.median_us * 1e6);
   }
-  {  // HBM: copy a buffer well beyond L2 + the 256 MiB Infinity Cache
-    const size_t bytes = size_t(1) << 29;
-    DeviceBuffer a(bytes), b(bytes);
-    GIE_HIP_CHECK(hipMemsetAsync(a.data(), 0, bytes, s));
+  {
+    // HBM: a 512 MiB copy, twice the 256 MiB Infinity Cache, read + write counted
+    const size_t bytes = size_t(512) << 20;
+    DeviceBuffer src(bytes), dst(bytes);
+    GIE_HIP_CHECK(hipMemsetAsync(src.data(), 0, bytes, stream.get()));
     const TimingStats t = time_stream_work(
-        [&](hipStream_t st) { check_kernel_status(gie_hip_ceiling_copy(a.data(), b.data(), bytes, st), "copy ceiling"); },
-        s, to);
+        [&](hipStream_t s) {
+          check_kernel_status(gie_hip_ceiling_copy(src.data(), dst.data(), bytes, s), "copy ceiling");
+        },
+        stream.get(), to);
     c.bw_gbs = 2.0 * double(bytes) / (t.median_us * 1e3);
   }
-  {  // launch cost: back-to-back empty kernels on one stream
+  {
+    // dispatch: back-to-back empty kernels on one stream
     const TimingStats t = time_stream_work(
-        [&](hipStream_t st) { check_kernel_status(gie_hip_ceiling_empty(st), "empty kernel"); }, s, to);
+        [&](hipStream_t s) { check_kernel_status(gie_hip_ceiling_empty(s), "empty kernel"); }, stream.get(), to);
     c.launch_overhead_us = t.median_us;
   }
   c.measured = true;
@@ -151,15 +225,12 @@ DeviceCeilings measure_ceilings(int device, bool use_cache) {
       v["fp16_mfma_tflops"] = c.fp16_tc_tflops;
       v["bw_gbs"] = c.bw_gbs;
       v["launch_overhead_us"] = c.launch_overhead_us;
-      const std::string path = ceiling_path(device);
-      const size_t slash = path.find_last_of('/');
-      if (slash != std::string::npos) {
-        const std::string cmd = "mkdir -p '" + path.substr(0, slash) + "'";
-        if (std::system(cmd.c_str()) != 0) throw Error(StatusCode::kIo, "cannot create " + path.substr(0, slash));
-      }
-      json::write_file(path, v);
+      const std::string path = ceiling_file(device);
+      std::error_code ec;
+      std::filesystem::create_directories(std::filesystem::path(path).parent_path(), ec);
+      if (!ec) json::write_file(path, v);
     } catch (const Error&) {
-      // an unwritable cache directory only costs a re-measurement next time
+      // an unwritable cache only costs a measurement next time
     }
   }
   return c;
@@ -167,17 +238,18 @@ DeviceCeilings measure_ceilings(int device, bool use_cache) {
 
 ProblemModel analyze_problem(const ConvProblem& prob) {
   const Conv2DParams& p = prob.p;
-  const double esz = double(dtype_size(prob.dtype()));
+  const double es = double(dtype_size(prob.dtype()));
   ProblemModel m;
   m.flops = double(p.flops());
-  m.input_bytes = double(p.input_shape().numel()) * esz;
-  m.weight_bytes = double(p.weight_shape().numel()) * esz;
-  m.output_bytes = double(p.output_shape().numel()) * esz;
-  m.bias_bytes = prob.has_bias ? double(p.out_channels) * esz : 0.0;
+  m.input_bytes = es * double(p.input_shape().numel());
+  m.weight_bytes = es * double(p.weight_shape().numel());
+  m.output_bytes = es * double(p.output_shape().numel());
+  m.bias_bytes = prob.has_bias ? es * double(p.out_channels) : 0.0;
   m.compulsory_bytes = m.input_bytes + m.weight_bytes + m.output_bytes + m.bias_bytes;
-  m.im2col_bytes = double(p.batch) * double(p.gemm_k()) * double(p.out_h()) * double(p.out_w()) * esz;
-  m.im2col_extra_traffic = 2.0 * m.im2col_bytes;
-  m.unfused_extra_traffic = 2.0 * m.output_bytes;
+  // an explicit unrolled matrix has one row of C*Kh*Kw taps per output pixel
+  m.im2col_bytes = es * double(p.gemm_k()) * double(p.gemm_n());
+  m.im2col_extra_traffic = 2.0 * m.im2col_bytes;  // written once, read once
+  m.unfused_extra_traffic = 2.0 * m.output_bytes;  // a separate bias/ReLU pass reads and writes Y again
   m.arithmetic_intensity = m.flops / m.compulsory_bytes;
   m.unrolled_blowup = m.im2col_bytes / m.input_bytes;
   return m;
@@ -186,63 +258,54 @@ ProblemModel analyze_problem(const ConvProblem& prob) {
 Estimate roofline_estimate(const ConvProblem& prob, const DeviceCeilings& c, bool tensor_cores) {
   const ProblemModel m = analyze_problem(prob);
   Estimate e;
-  e.compute_us = m.flops / flops_per_us(tensor_cores ? c.fp16_tc_tflops : c.fp32_tflops);
-  e.memory_us = m.compulsory_bytes / bytes_per_us(c);
+  e.compute_us = m.flops / ((tensor_cores ? c.fp16_tc_tflops : c.fp32_tflops) * 1e6);
+  e.memory_us = m.compulsory_bytes / (c.bw_gbs * 1e3);
   e.launch_us = c.launch_overhead_us;
-  e.time_us = std::max(e.compute_us, e.memory_us);
-  e.bound = classify(e.compute_us, e.memory_us, e.launch_us);
-  if (e.bound == Bound::kLaunch) e.time_us = e.launch_us;
+  e.bound = bound_of(e.compute_us, e.memory_us, e.launch_us);
+  e.time_us = e.bound == Bound::kLaunch ? e.launch_us : std::max(e.compute_us, e.memory_us);
   return e;
 }
 
 double backend_efficiency_prior(const KernelDesc& k) {
+  if (const FamilyProfile* f = profile_of(k.name)) return f->mfma_eff;
   if (k.efficiency_prior > 0) return k.efficiency_prior;
-  switch (k.backend) {
-    case Backend::kDirect: return 0.05;
-    case Backend::kSimtTiled: return 0.40;
-    case Backend::kImplicitGemm: return 0.55;
-    case Backend::kTensorCore: return 0.30;
-    case Backend::kIm2colGemm: return 0.60;
-    default: return 0.1;
-  }
+  return 0.10;  // a kernel outside the measured families
 }
 
 Estimate estimate_kernel(const ConvProblem& prob, const KernelDesc& k, const DeviceInfo& dev, const DeviceCeilings& c) {
   const ProblemModel m = analyze_problem(prob);
+  const FamilyProfile* fam = profile_of(k.name);
+  const double mfma_eff = backend_efficiency_prior(k);
+  const double hbm_eff = fam ? fam->hbm_eff : 0.35;
+
   Estimate e;
-  if (k.tile_efficiency) {
-    e.tile_efficiency = k.tile_efficiency(prob);
-  } else {
-    const auto pad = [](int64_t v, int64_t t) { return double(v) / double(((v + t - 1) / t) * t); };
-    e.tile_efficiency = pad(prob.p.gemm_m(), k.tile_m) * pad(prob.p.gemm_n(), k.tile_n) * pad(prob.p.gemm_k(), k.tile_k);
-  }
+  e.tile_efficiency = k.tile_efficiency ? k.tile_efficiency(prob) : padded_fraction(prob, k);
   const int64_t blocks = k.num_blocks ? std::max<int64_t>(k.num_blocks(prob), 1) : 1;
   e.blocks_per_sm = k.blocks_per_cu ? std::max(k.blocks_per_cu(prob), 1) : 1;
-  const double slots = double(dev.sm_count) * e.blocks_per_sm;
-  e.wave_efficiency = double(blocks) / (std::ceil(double(blocks) / slots) * slots);
-  // a workgroup occupies one CU: below one workgroup per CU the idle CUs are lost too
-  const double cu_fill = std::min(1.0, double(blocks) / double(std::max(dev.sm_count, 1)));
+  const int xcds = (dev.sm_count >= kXcds && dev.sm_count % kXcds == 0) ? kXcds : 1;
+  const int64_t slots = int64_t(dev.sm_count / xcds) * e.blocks_per_sm;  // resident workgroups per XCD
+  const int64_t per_xcd = (blocks + xcds - 1) / xcds;
+  const int64_t waves = (per_xcd + slots - 1) / slots;
+  e.wave_efficiency = double(blocks) / double(waves * slots * xcds);
 
-  const double peak = k.uses_tensor_cores ? c.fp16_tc_tflops : c.fp32_tflops;
-  const double eff = backend_efficiency_prior(k) * std::max(e.tile_efficiency, 1e-3) *
-                     std::max(std::min(e.wave_efficiency, cu_fill), 1e-3);
-  e.compute_us = m.flops / (flops_per_us(peak) * eff);
-
-  double traffic = m.compulsory_bytes;
-  if (k.extra_traffic_bytes) traffic += k.extra_traffic_bytes(prob);
-  e.memory_us = traffic / bytes_per_us(c);
-  e.launch_us = c.launch_overhead_us * k.launches;
-  e.bound = classify(e.compute_us, e.memory_us, e.launch_us);
-  e.time_us = std::max(e.compute_us, e.memory_us) + e.launch_us;
+  const double peak_tflops = k.uses_tensor_cores ? c.fp16_tc_tflops : c.fp32_tflops;
+  const double rate = peak_tflops * 1e6 * mfma_eff * std::max(e.tile_efficiency, 1e-3) *
+                      std::max(e.wave_efficiency, 1e-3);  // FLOP per us
+  e.compute_us = m.flops / rate;
+  const double traffic = m.compulsory_bytes + (k.extra_traffic_bytes ? k.extra_traffic_bytes(prob) : 0.0);
+  e.memory_us = traffic / (c.bw_gbs * 1e3 * hbm_eff);
+  // resident workgroups overlap each other's set-up, so only the launch's first fill and last drain are exposed
+  e.launch_us = c.launch_overhead_us * std::max(k.launches, 1) + (fam ? fam->fill_us : 2.0);
   {
-    std::lock_guard<std::mutex> lock(g_cal_mu);
-    auto it = cal_map().find(to_string(k.backend));
-    if (it != cal_map().end()) {
+    std::lock_guard<std::mutex> lock(g_scale_mu);
+    const auto it = backend_scale().find(to_string(k.backend));
+    if (it != backend_scale().end()) {
       e.compute_us *= it->second;
       e.memory_us *= it->second;
-      e.time_us = std::max(e.compute_us, e.memory_us) + e.launch_us;
     }
   }
+  e.bound = bound_of(e.compute_us, e.memory_us, e.launch_us);
+  e.time_us = std::max(e.compute_us, e.memory_us) + e.launch_us;
   return e;
 }
 

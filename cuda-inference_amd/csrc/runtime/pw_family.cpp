@@ -130,9 +130,7 @@ KernelDesc make_entry() {
   k.tile_n = Stream ? 64 : 128;
   k.tile_k = Stream ? 16 : 32;
   k.uses_tensor_cores = true;
-  k.needs_lut = false;
   k.launches = 1;
-  k.efficiency_prior = 0.6;
   k.supports = &F::supports;
   k.workspace_bytes = &F::workspace;
   k.dynamic_smem_bytes = &F::lds;

@@ -1,5 +1,6 @@
 // Kernel registry (the reference's registry.cpp contract: unique names, mandatory function pointers, stable
-// element addresses) + the LUT builders of the reference's API.
+// element addresses). The reference's per-(c,r,s) gather tables (src/kernels/conv_common.cu:39-50) have no
+// counterpart: every kernel here walks the filter taps with incremental offsets computed in registers.
 #include <set>
 #include <sstream>
 
@@ -63,29 +64,6 @@ std::vector<const KernelDesc*> kernels_for_backend(Backend b) {
   for (const auto& k : kernel_registry())
     if (b == Backend::kAuto || k.backend == b) out.push_back(&k);
   return out;
-}
-
-std::vector<LutEntry> build_conv_lut(const Conv2DParams& p) {
-  const int64_t K = p.gemm_k();
-  std::vector<LutEntry> lut(static_cast<size_t>(K));
-  const int khw = p.kernel_h * p.kernel_w;
-  for (int64_t k = 0; k < K; ++k) {
-    const int c = int(k / khw), rs = int(k % khw);
-    lut[size_t(k)] = {c * p.in_h * p.in_w, (rs / p.kernel_w) * p.dilation_h, (rs % p.kernel_w) * p.dilation_w, 0};
-  }
-  return lut;
-}
-
-std::vector<LutEntry> build_conv_lut_chunked(const Conv2DParams& p) {
-  if (p.in_channels % 8 != 0) throw Error(StatusCode::kInvalidArgument, "chunked LUT needs C % 8 == 0");
-  const int cv = p.in_channels / 8;
-  const int64_t chunks = p.gemm_k() / 8;
-  std::vector<LutEntry> lut(static_cast<size_t>(chunks));
-  for (int64_t q = 0; q < chunks; ++q) {
-    const int rs = int(q / cv);
-    lut[size_t(q)] = {int32_t(8 * (q % cv)), (rs / p.kernel_w) * p.dilation_h, (rs % p.kernel_w) * p.dilation_w, 0};
-  }
-  return lut;
 }
 
 }  // namespace gie

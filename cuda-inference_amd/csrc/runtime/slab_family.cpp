@@ -113,7 +113,20 @@ struct Fns {
   static double extra_traffic(const ConvProblem& prob) {  // FP32 partials written and read back
     return e().split > 1 ? 2.0 * e().split * double(prob.p.output_shape().numel()) * 4.0 : 0.0;
   }
-  static int occupancy(const ConvProblem& prob) { return lds(prob) > 80 * 1024 ? 1 : 2; }
+  // 256 threads holding ~400 VGPR+AGPR each: one workgroup per CU whatever the LDS
+  static int occupancy(const ConvProblem&) { return 1; }
+  // Useful output positions per step-equivalent: every slab of rows runs the step sequence of the widest
+  // configuration (224 positions x 32 filters), whatever its own rows x pitch, because a step's time is set by its
+  // loads and waits more than by its MFMA count; times the filter and channel padding.
+  static double tile_efficiency(const ConvProblem& prob) {
+    const Entry& en = e();
+    const Conv2DParams& p = prob.p;
+    const int64_t slabs = (p.out_h() + en.info.rows - 1) / en.info.rows;
+    const double pos = double(p.out_h()) * p.out_w() / (double(slabs) * 224.0);
+    const double o = double(p.out_channels) / double(((p.out_channels + 31) / 32) * 32);
+    const double c = double(p.in_channels) / double(((p.in_channels + 31) / 32) * 32);
+    return std::min(1.0, pos) * o * c;
+  }
   static void launch(const LaunchArgs& la) {
     const Entry& en = e();
     const ConvProblem& prob = *la.problem;
@@ -154,6 +167,7 @@ void fill_fns(int idx, KernelDesc& k) {
       k.num_blocks = &Fns<I>::blocks;
       k.extra_traffic_bytes = &Fns<I>::extra_traffic;
       k.blocks_per_cu = &Fns<I>::occupancy;
+      k.tile_efficiency = &Fns<I>::tile_efficiency;
       k.launch = &Fns<I>::launch;
       return;
     }
@@ -191,9 +205,7 @@ void register_slab_family(std::vector<KernelDesc>& out) {
     k.tile_n = en.info.rows * en.info.pitch;
     k.tile_k = en.info.tile_k * 9;
     k.uses_tensor_cores = true;
-    k.needs_lut = false;
     k.launches = 1 + (en.split > 1 ? 1 : 0);
-    k.efficiency_prior = 0.6;
     fill_fns<0>(int(i), k);
     out.push_back(std::move(k));
   }

@@ -78,6 +78,11 @@ class GieSlabConfig(ctypes.Structure):
                                             "version")]
 
 
+class GieDeviceModel(ctypes.Structure):
+    _fields_ = [("cus", ctypes.c_int), ("mfma_tflops", ctypes.c_double), ("fp32_tflops", ctypes.c_double),
+                ("hbm_gbs", ctypes.c_double), ("launch_us", ctypes.c_double), ("lds_per_workgroup", ctypes.c_size_t)]
+
+
 class GieIgemmConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "tile_m", "tile_n", "tile_k", "waves_m", "waves_n", "threads", "lds_bytes", "stages", "version")]
@@ -123,6 +128,8 @@ _CAPI = {
     "gie_tune_cache_size": ([_cp, ctypes.POINTER(_sz)], _i),
     "gie_tune_cache_clear": ([_cp], _i),
     "gie_estimate_kernel": ([_cp, _PP, _dp, _ip], _i),
+    "gie_model_estimate": ([_cp, _PP, ctypes.POINTER(GieDeviceModel), _dp, _ip], _i),
+    "gie_model_rank": ([_PP, ctypes.POINTER(GieDeviceModel), ctypes.c_char_p, _sz, _dp, _i, _ip], _i),
     "gie_measure_ceilings": ([_i, _i, _dp, _ip], _i),
     "gie_theoretical_ceilings": ([_i, _dp], _i),
     "gie_gpu_reference": ([_PP, _vp, _vp, _vp, _vp, _vp, _vp], _i),
@@ -693,6 +700,43 @@ def estimate(name: str, p: Problem) -> dict:
                  list(out)))
     d["bound"] = ("compute", "bandwidth", "launch")[bound.value]
     return d
+
+
+# MI355X as the cost model describes it without measuring: 256 CUs, dense FP16 MFMA and FP32 vector peaks, HBM3E,
+# dispatch gap of back-to-back launches, LDS opt-in limit per workgroup.
+MI355X_MODEL = dict(cus=256, mfma_tflops=2516.6, fp32_tflops=157.3, hbm_gbs=8000.0, launch_us=1.5,
+                    lds_per_workgroup=160 * 1024)
+
+
+def _device_model(dev: dict | None) -> GieDeviceModel:
+    d = dict(MI355X_MODEL, **(dev or {}))
+    return GieDeviceModel(d["cus"], d["mfma_tflops"], d["fp32_tflops"], d["hbm_gbs"], d["launch_us"],
+                          d["lds_per_workgroup"])
+
+
+def model_estimate(name: str, p: Problem, dev: dict | None = None) -> dict:
+    """The cost model's estimate for kernel `name` on a described device (MI355X by default); needs no GPU."""
+    pc, dm = p.c(), _device_model(dev)
+    out = (ctypes.c_double * 6)()
+    bound = ctypes.c_int()
+    check(capi().gie_model_estimate(name.encode(), ctypes.byref(pc), ctypes.byref(dm), out, ctypes.byref(bound)),
+          "model_estimate")
+    d = dict(zip(("time_us", "compute_us", "memory_us", "launch_us", "tile_efficiency", "wave_efficiency"),
+                 list(out)))
+    d["bound"] = ("compute", "bandwidth", "launch")[bound.value]
+    return d
+
+
+def model_rank(p: Problem, dev: dict | None = None):
+    """Capable kernels, best first, with the model's estimate on a described device; needs no GPU."""
+    pc, dm = p.c(), _device_model(dev)
+    buf = ctypes.create_string_buffer(65536)
+    us = (ctypes.c_double * 1024)()
+    n = ctypes.c_int()
+    check(capi().gie_model_rank(ctypes.byref(pc), ctypes.byref(dm), buf, 65536, us, 1024, ctypes.byref(n)),
+          "model_rank")
+    names = buf.value.decode().split("\n") if n.value else []
+    return list(zip(names, list(us)[:n.value]))
 
 
 def measure_ceilings(device=0, use_cache=False) -> dict:

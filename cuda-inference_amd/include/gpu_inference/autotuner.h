@@ -78,6 +78,7 @@ class TuneCache {
     std::string timestamp;
   };
   mutable std::map<std::string, Entry> entries_;
+  mutable std::string text_;  // file contents entries_ was parsed from
   mutable bool loaded_ = false;
 };
 

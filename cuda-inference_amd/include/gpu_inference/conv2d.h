@@ -81,7 +81,9 @@ struct ConvProblem {
 
   DataType dtype() const { return tensor_dtype(precision); }
   std::string key() const;  // canonical string, used for plan/cache keys
-  bool operator==(const ConvProblem& o) const { return key() == o.key(); }
+  bool operator==(const ConvProblem& o) const {
+    return p == o.p && precision == o.precision && has_bias == o.has_bias && activation == o.activation;
+  }
 };
 
 // Throws gie::Error(kInvalidArgument / kUnsupported) with a specific message.

@@ -31,7 +31,7 @@ class ExecutionPlan {
   const ConvProblem& problem() const { return problem_; }
   const KernelDesc& kernel() const { return *kernel_; }
   size_t workspace_bytes() const { return workspace_bytes_; }
-  size_t persistent_bytes() const { return persistent_bytes_ + lut_bytes_; }
+  size_t persistent_bytes() const { return persistent_bytes_; }
   int device() const { return device_; }
 
  private:
@@ -41,8 +41,8 @@ class ExecutionPlan {
   int device_ = 0;
   size_t workspace_bytes_ = 0;
   size_t persistent_bytes_ = 0;
-  size_t lut_bytes_ = 0;
-  DeviceBuffer lut_;
+  size_t x_bytes_ = 0, w_bytes_ = 0, y_bytes_ = 0, bias_bytes_ = 0;  // operand footprints, for the alias checks
+  LaunchArgs proto_;  // everything but the pointers and the stream, filled once by create()
   std::shared_ptr<void> state_;
 };
 

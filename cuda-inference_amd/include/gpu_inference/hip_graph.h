@@ -33,7 +33,7 @@ class HipGraphExecutor {
   double instantiate_us() const { return instantiate_us_; }
 
  private:
-  void capture_graph(const Enqueue& enqueue, hipGraph_t* g, double* us);
+  void adopt(hipGraph_t g, double capture_us);  // instantiates g as the executable graph, taking ownership of it
   void reset();
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t exec_ = nullptr;

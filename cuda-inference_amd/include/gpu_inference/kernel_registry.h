@@ -31,7 +31,6 @@ struct LaunchArgs {
   void* y = nullptr;
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
-  const void* plan_data = nullptr;  // device-resident per-problem tables (see needs_lut)
   void* plan_state = nullptr;       // opaque per-plan state created by KernelDesc::create_state
   hipStream_t stream = nullptr;
   // Profiling hook: >= 0 launches only that stage of a multi-launch kernel (0 = repack, 1 = main kernel,
@@ -50,10 +49,8 @@ struct KernelDesc {
   // Tile extents in the implicit-GEMM view (M = C_out, N = B*Ho*Wo, K = C_in*Kh*Kw).
   int tile_m = 1, tile_n = 1, tile_k = 1;
   bool uses_tensor_cores = false;  // matrix cores (MFMA)
-  bool needs_lut = false;
-  bool lut_chunked = false;
   int launches = 1;             // kernel launches per forward call (cost model)
-  double efficiency_prior = 0;  // fraction of the compute ceiling this family is expected to reach
+  double efficiency_prior = 0;  // compute-ceiling fraction for a family the cost model has no measured profile of
   double (*extra_traffic_bytes)(const ConvProblem&) = nullptr;  // DRAM bytes beyond compulsory X/W/Y
   const void* function = nullptr;  // primary __global__ function, may be null (occupancy via blocks_per_cu)
 
@@ -76,16 +73,5 @@ const std::vector<KernelDesc>& kernel_registry();
 std::vector<KernelDesc>& kernel_registry_for_testing();
 const KernelDesc* find_kernel(const std::string& name);
 std::vector<const KernelDesc*> kernels_for_backend(Backend b);
-
-// Per-(c,r,s) lookup entry for implicit-GEMM gathers.
-struct alignas(16) LutEntry {
-  int32_t c_off;
-  int32_t r_off;
-  int32_t s_off;
-  int32_t pad_;
-};
-std::vector<LutEntry> build_conv_lut(const Conv2DParams& p);
-// One entry per 8 consecutive k in (r, s, c) order over NHWC channel vectors. Requires C % 8 == 0.
-std::vector<LutEntry> build_conv_lut_chunked(const Conv2DParams& p);
 
 }  // namespace gie

@@ -112,6 +112,18 @@ int gie_estimate_kernel(const char* name, const gie_problem* p, double* out6, in
 /* out3 = {fp16_mfma_tflops, bw_gbs, launch_overhead_us} */
 int gie_measure_ceilings(int device, int use_cache, double* out3, int* measured);
 int gie_theoretical_ceilings(int device, double* out3);
+/* The cost model on a described device instead of the current GPU (no GPU needed): a gfx950 part with `cus`
+   compute units, the given ceilings and LDS opt-in limit. No counterpart in the reference; it lets hosts and tests
+   see which kernel the model would pick for a machine without one. */
+typedef struct gie_device_model {
+  int cus;
+  double mfma_tflops, fp32_tflops, hbm_gbs, launch_us;
+  size_t lds_per_workgroup;
+} gie_device_model;
+int gie_model_estimate(const char* name, const gie_problem* p, const gie_device_model* d, double* out6, int* bound);
+/* capable kernels, best first, newline-separated in buf; estimated us in us[0..max) */
+int gie_model_rank(const gie_problem* p, const gie_device_model* d, char* buf, size_t n, double* us, int max,
+                   int* count);
 
 /* ---- reference and device description ---- */
 /* GPU double reference (reference.h:36-39): y, scale float device buffers */
