@@ -41,6 +41,10 @@ CONFIGS = {
                                stride_h=1, stride_w=1, pad_h=1, pad_w=1, precision="bf16"),
 }
 HEADLINE = "c2_fp16_3x3"
+# the reference's CPU-runnable FP32 case (timed on the host only)
+C1 = dict(batch=1, in_channels=64, in_h=56, in_w=56, out_channels=64, kernel_h=3, kernel_w=3, stride_h=1, stride_w=1,
+          pad_h=1, pad_w=1, precision="fp32")
+SPLITK = "c5_bf16_3x3_splitk"
 
 
 def log(msg):
@@ -93,12 +97,10 @@ def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
     cb = compulsory_bytes(p)
     ai = flops / cb
     roof_tflops = min(PEAK_FP16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
-    cp = (p.in_channels + 31) // 32 * 32 if kernel.startswith("halo_") else (p.in_channels + 7) // 8 * 8
-    repack_bytes = float((np.prod(p.x_shape()) + np.prod(p.w_shape())) * 2 +
-                         (p.batch * p.in_h * p.in_w + p.out_channels * p.kernel_h * p.kernel_w) * cp * 2)
     desc = gie.kernel_describe(kernel)
     split = desc.get("split_k", 1)
-    reduce_bytes = float(split * np.prod(p.y_shape()) * 4 + np.prod(p.y_shape()) * 2) if split > 1 else 0.0
+    rp_bytes = repack_bytes(kernel, p)
+    rd_bytes = reduce_bytes(split, p)
     out = {
         "kernel": kernel, "selection": source, "gemm_view": {"M": p.gemm_m, "N": p.gemm_n, "K": p.gemm_k},
         "gflop": flops / 1e9, "us_per_call": us_call, "tflops": tflops,
@@ -107,12 +109,88 @@ def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
         "bound": "mfma" if ai * PEAK_HBM_GBS / 1e3 >= PEAK_FP16_TFLOPS else "hbm",
         "compulsory_mb": cb / 1e6, "arith_intensity": ai,
         "stage_us": stages, "gemm_kernel_tflops": gemm_tflops,
-        "repack_gbs": repack_bytes / (stages["repack_us"] * 1e-6) / 1e9 if stages["repack_us"] > 0 else None,
-        "reduce_gbs": reduce_bytes / (stages["reduce_us"] * 1e-6) / 1e9 if stages["reduce_us"] > 0 else None,
+        "repack_bytes": rp_bytes, "reduce_bytes": rd_bytes,
+        "repack_gbs": rp_bytes / (stages["repack_us"] * 1e-6) / 1e9 if rp_bytes else None,
+        "reduce_gbs": rd_bytes / (stages["reduce_us"] * 1e-6) / 1e9 if rd_bytes else None,
         "split_k": split, "rel_l2": rel_l2, "max_abs": max_abs,
         "parity_ok": bool(rel_l2 <= 1e-3 and max_abs <= 2e-2),
     }
     return p, t, out
+
+
+def repack_bytes(kernel: str, p):
+    """HBM bytes the kernel's repack launch moves (reads of x/w plus writes of the repacked copies), or None for a
+    family that has no repack launch (slab, pw, stem and narrow read NCHW x and OIHW w directly)."""
+    e = p.esize
+    nx, nw = float(np.prod(p.x_shape())), float(np.prod(p.w_shape()))
+    taps = p.kernel_h * p.kernel_w
+    if kernel.startswith("band_"):  # weights only: OIHW -> 32-channel blocks
+        cp = (p.in_channels + 31) // 32 * 32
+        return (nw + p.out_channels * taps * cp) * e
+    if kernel.startswith("halo_") or kernel.startswith("mfma_"):  # x -> NHWC, w -> O x taps x C, channels padded
+        cp = (p.in_channels + 31) // 32 * 32 if kernel.startswith("halo_") else (p.in_channels + 7) // 8 * 8
+        return (nx + nw + (p.batch * p.in_h * p.in_w + p.out_channels * taps) * cp) * e
+    return None
+
+
+def reduce_bytes(split: int, p):
+    """HBM bytes of the split-K reduce (FP32 partials read, bias read, output written), None without split-K."""
+    if split <= 1:
+        return None
+    ny = float(np.prod(p.y_shape()))
+    return split * ny * 4 + ny * p.esize + p.out_channels * p.esize
+
+
+def fastest_split_entry(gie, cfg, stream):
+    """Among the registry entries with split_k > 1 that can run cfg, the fastest by a short plan timing."""
+    p = gie.Problem(**cfg, has_bias=True, relu=True)
+    x, w, b = gie.make_host_data(p, SEED, "uniform", "benchmark")
+    t = gie.ConvTensors(p, x, w, b)
+    best, best_us = None, float("inf")
+    for name in gie.registry():
+        if gie.kernel_describe(name).get("split_k", 1) <= 1 or not gie.kernel_supports(name, p)[0]:
+            continue
+        plan = gie.Plan(p, name)
+        ws = gie.DeviceBuffer(plan.workspace_bytes)
+        us = plan.time(t, ws, stream, warmup=3, samples=5, min_sample_ms=0.3)["median_us"]
+        if us < best_us:
+            best, best_us = name, us
+    return best
+
+
+def cpu_time(c, x, w, b, cores: int, min_runs: int, budget_s: float):
+    """Median wall time of the oracle on (c, x, w, b): at least min_runs runs, more while within budget_s."""
+    import oracle as O
+    times = []
+    t_end = time.time() + budget_s
+    while len(times) < min_runs or (time.time() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        O.conv2d(c, x, w, b, threads=cores)
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_configs(budget_s: float):
+    """The oracle on BASELINE configs 1 (FP32, N=1 C=64 56x56 K=64 3x3) and 3-5, full workloads, median of >= 5
+    (config 1) or >= 3 runs, on this host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    cores = len(os.sched_getaffinity(0))
+    out = {}
+    for name, cfg, runs in (("c1_fp32_3x3", C1, 5), ("c3_fp16_1x1", CONFIGS["c3_fp16_1x1"], 3),
+                            ("c4_fp16_7x7s2_stem", CONFIGS["c4_fp16_7x7s2_stem"], 3),
+                            ("c5_bf16_3x3_splitk", CONFIGS["c5_bf16_3x3_splitk"], 3)):
+        c = O.Conv(cfg["batch"], cfg["in_channels"], cfg["in_h"], cfg["in_w"], cfg["out_channels"], cfg["kernel_h"],
+                   cfg["kernel_w"], cfg["stride_h"], cfg["stride_w"], cfg["pad_h"], cfg["pad_w"], has_bias=True,
+                   relu=True, precision=cfg["precision"])
+        x, w, b = O.make_data(c, SEED, O.UNIFORM, O.SCALING_BENCH)
+        med, n = cpu_time(c, x, w, b, cores, runs, budget_s)
+        flops = 2.0 * cfg["batch"] * cfg["out_channels"] * c.out_h * c.out_w * cfg["in_channels"] * cfg["kernel_h"] * \
+            cfg["kernel_w"]
+        out[name] = {"us_per_call": med * 1e6, "tflops": flops / med / 1e12, "runs": n, "cores": cores,
+                     "precision": cfg["precision"]}
+        log(f"[bench] cpu {name}: {med * 1e3:.2f} ms/call ({n} runs, {cores} threads)")
+    return out
 
 
 def cpu_baseline(p, t, budget_s: float):
@@ -123,18 +201,10 @@ def cpu_baseline(p, t, budget_s: float):
                p.stride_w, p.pad_h, p.pad_w, has_bias=True, relu=True, precision=p.precision)
     x, w, b = O.make_data(c, SEED, O.UNIFORM, O.SCALING_BENCH)
     cores = len(os.sched_getaffinity(0))
-    times = []
-    t_end = time.time() + budget_s
-    while True:
-        t0 = time.perf_counter()
-        O.conv2d(c, x, w, b, threads=cores)
-        times.append(time.perf_counter() - t0)
-        if time.time() > t_end or len(times) >= 50:
-            break
-    med = float(np.median(times))
+    med, n = cpu_time(c, x, w, b, cores, 5, budget_s)
     return {"value": p.flops() / med / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "us_per_call": med * 1e6,
-            "sample": f"full config-2 workload ({p.flops() / 1e9:.2f} GFLOP) x {len(times)} runs, median; "
+            "sample": f"full config-2 workload ({p.flops() / 1e9:.2f} GFLOP) x {n} runs, median; "
                       f"oracle/gie_oracle.c cpu_conv2d_reference restatement, {cores} OpenMP threads",
             "cpu_model": _cpu_model()}
 
@@ -205,7 +275,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--tune-cache", default=os.path.join(ROOT, "gpurun_out", "bench_tune_cache.json"))
     ap.add_argument("--kernel", default=None,
-                    help="force this registry kernel (no autotune); only with a single --configs entry")
+                    help="force this registry kernel (no autotune) on a single --configs entry; for a config other "
+                         "than the headline only that config runs and its result dict is printed (profiling runs)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -222,8 +293,14 @@ def main():
         return
     stream = gie.Stream()
     names = list(CONFIGS) if args.configs == "all" else args.configs.split(",")
-    if args.kernel and names != [HEADLINE]:
-        ap.error(f"--kernel applies to --configs {HEADLINE} alone")
+    if args.kernel and len(names) != 1:
+        ap.error("--kernel applies to a single --configs entry")
+    if args.kernel and names[0] != HEADLINE:
+        name = names[0]
+        _, _, r = run_config(gie, name, CONFIGS[name], args.steps, args.warmup, stream, args.tune_cache, args.kernel)
+        log(f"[bench] {name}: {r['kernel']} {r['us_per_call']:.2f} us/call (kernel {r['stage_us']['gemm_us']:.2f} us)")
+        print(json.dumps({"config": name, "result": r}), flush=True)
+        return
     if HEADLINE not in names:
         names.insert(0, HEADLINE)
     results = {}
@@ -232,19 +309,37 @@ def main():
         log(f"[bench] {name}: tuning + timing")
         steps = args.steps if name == HEADLINE else max(100, args.steps // 4)
         p, t, r = run_config(gie, name, CONFIGS[name], steps, args.warmup if name == HEADLINE else 50, stream,
-                             args.tune_cache, args.kernel)
+                             args.tune_cache, args.kernel if name == HEADLINE else None)
         log(f"[bench] {name}: {r['kernel']} {r['us_per_call']:.2f} us/call {r['tflops']:.1f} TFLOP/s "
             f"(gemm {r['stage_us']['gemm_us']:.2f} us, repack {r['stage_us']['repack_us']:.2f} us) "
             f"rel_l2={r['rel_l2']:.2e}")
         results[name] = r
         if name == HEADLINE:
             head = (p, t)
+    if SPLITK in names and not args.kernel:
+        # BASELINE config 5 is the split-K config: whatever the autotuner picked, also bench the fastest entry that
+        # splits the reduction, so the reduce kernel's time and GB/s are measured on the real shape
+        best = fastest_split_entry(gie, CONFIGS[SPLITK], stream)
+        if best:
+            log(f"[bench] {SPLITK}: forced split-K entry {best}")
+            _, _, r = run_config(gie, SPLITK, CONFIGS[SPLITK], max(100, args.steps // 4), 50, stream,
+                                 args.tune_cache, best)
+            r["selection"] = "forced: fastest split_k > 1 entry by a short plan timing"
+            log(f"[bench] {SPLITK} split-K: {r['kernel']} {r['us_per_call']:.2f} us/call, reduce "
+                f"{r['stage_us']['reduce_us']:.2f} us = {r['reduce_gbs'] or 0:.0f} GB/s")
+            results[SPLITK + "_forced_splitk"] = r
     hr = results[HEADLINE]
     p, t = head
     cpu = None
+    cpu_other = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline (oracle) on the host")
         cpu = cpu_baseline(p, t, args.cpu_budget_s)
+        cpu_other = cpu_configs(min(args.cpu_budget_s, 5.0))
+        cpu["other_configs"] = cpu_other
+    host = gie.measure_host_cost(gie.Problem(1, 8, 8, 8, 8, 3, 3, 1, 1, 1, 1, precision="fp16"), 256)
+    log(f"[bench] host cost per Conv2D::forward (plan cached, 1x8x8x8 -> 8 3x3): {host['host_us_per_forward']:.2f} "
+        f"us vs {host['host_us_per_bare_launch']:.2f} us per bare kernel launch")
     gemm_us = hr["stage_us"]["gemm_us"]
     achieved = p.flops() / (gemm_us * 1e-6) / 1e12
     line = {
@@ -260,6 +355,7 @@ def main():
                      "kernel": dominant_kernel(hr["kernel"]), "avg_launch_us": gemm_us,
                      "flop_per_launch": p.flops()},
         "cpu_baseline": cpu,
+        "host_cost": host,
         "parity": {"rel_l2": hr["rel_l2"], "max_abs": hr["max_abs"], "ok": hr["parity_ok"],
                    "against": "library GPU double reference on the timed call's inputs"},
         "configs": results,

@@ -6,7 +6,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
+#include <functional>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -211,6 +213,66 @@ int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_te
     for (int i = 0; i < count; ++i)
       Conv2D::forward(xr, wr, bias ? &b : nullptr, pr, yr, workspace, workspace_bytes,
                       static_cast<hipStream_t>(stream), o);
+  });
+}
+
+int gie_measure_host_cost(const gie_problem* p, const gie_options* opt, int batch, double* out3) {
+  return guarded([&] {
+    GIE_REQUIRE(p != nullptr && out3 != nullptr && batch > 0, StatusCode::kInvalidArgument,
+                "host cost: null problem/output or batch <= 0");
+    const ConvProblem pr = to_problem(p);
+    const Conv2DOptions o = to_options(opt);
+    const Conv2DParams& q = pr.p;
+    const DataType dt = pr.dtype();
+    const size_t es = dtype_size(dt);
+    DeviceBuffer x(size_t(q.input_shape().numel()) * es), w(size_t(q.weight_shape().numel()) * es),
+        b(size_t(q.out_channels) * es), y(size_t(q.output_shape().numel()) * es);
+    GIE_HIP_CHECK(hipMemset(x.data(), 0, x.size()));
+    GIE_HIP_CHECK(hipMemset(w.data(), 0, w.size()));
+    GIE_HIP_CHECK(hipMemset(b.data(), 0, b.size()));
+    const size_t wsb = Conv2D::workspace_size(pr, o);
+    DeviceBuffer ws(wsb);
+    hipStream_t s = nullptr;
+    GIE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    struct Done {
+      hipStream_t s;
+      ~Done() { (void)hipStreamDestroy(s); }
+    } done{s};
+    const ConstTensorRef xr{x.data(), dt, q.input_shape()}, wr{w.data(), dt, q.weight_shape()},
+        br{b.data(), dt, q.bias_shape()};
+    const TensorRef yr{y.data(), dt, q.output_shape()};
+    auto forward = [&] { Conv2D::forward(xr, wr, pr.has_bias ? &br : nullptr, pr, yr, ws.data(), wsb, s, o); };
+    auto empty = [&] { check_kernel_status(gie_hip_ceiling_empty(s), "empty kernel"); };
+    // host wall time to enqueue `batch` calls (a batch well below the queue depth never waits for the GPU),
+    // median of 9 batches; the GPU time of the same batch from events on the stream
+    auto measure = [&](const std::function<void()>& call, double* host_us, double* dev_us) {
+      for (int i = 0; i < 32; ++i) call();
+      GIE_HIP_CHECK(hipStreamSynchronize(s));
+      std::vector<double> h, d;
+      hipEvent_t e0, e1;
+      GIE_HIP_CHECK(hipEventCreate(&e0));
+      GIE_HIP_CHECK(hipEventCreate(&e1));
+      for (int rep = 0; rep < 9; ++rep) {
+        GIE_HIP_CHECK(hipEventRecord(e0, s));
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < batch; ++i) call();
+        const auto t1 = std::chrono::steady_clock::now();
+        GIE_HIP_CHECK(hipEventRecord(e1, s));
+        GIE_HIP_CHECK(hipEventSynchronize(e1));
+        float ms = 0;
+        GIE_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        h.push_back(std::chrono::duration<double, std::micro>(t1 - t0).count() / batch);
+        d.push_back(1000.0 * ms / batch);
+      }
+      (void)hipEventDestroy(e0);
+      (void)hipEventDestroy(e1);
+      std::sort(h.begin(), h.end());
+      std::sort(d.begin(), d.end());
+      *host_us = h[h.size() / 2];
+      if (dev_us) *dev_us = d[d.size() / 2];
+    };
+    measure(forward, &out3[0], &out3[2]);
+    measure(empty, &out3[1], nullptr);
   });
 }
 

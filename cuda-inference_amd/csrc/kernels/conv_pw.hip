@@ -647,14 +647,6 @@ int pws_prepare(const gie_conv_geom* gg, int cu_count, PwsGeom* g, int* ks) {
   return GIE_HIP_OK;
 }
 
-int device_cu_count() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 256;
-  return cus;
-}
-
 }  // namespace
 }  // namespace gie_hip
 
@@ -703,7 +695,7 @@ extern "C" int gie_hip_conv_pws(int dtype, const gie_conv_geom* gg, const void* 
   if (bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) return GIE_HIP_EINVAL;
   PwsGeom g;
   int ks = 0;
-  if (int rc = pws_prepare(gg, device_cu_count(), &g, &ks)) return rc;
+  if (int rc = pws_prepare(gg, current_device_cus(), &g, &ks)) return rc;
   // 16-byte chunks into LDS, 16-byte weight loads, 8-byte stores
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
       (reinterpret_cast<uintptr_t>(y) & 7u))

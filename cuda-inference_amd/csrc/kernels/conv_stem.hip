@@ -361,14 +361,6 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
   return GIE_HIP_OK;
 }
 
-int device_cus() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 256;
-  return cus;
-}
-
 using StemFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, StemGeom);
 
 template <typename E, int R, bool RELU>
@@ -404,7 +396,7 @@ extern "C" int gie_hip_conv_stem(int dtype, const gie_conv_geom* gg, const void*
   if (bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) return GIE_HIP_EINVAL;
   StemGeom g;
   int lds = 0;
-  if (int rc = stem_prepare(gg, device_cus(), &g, &lds)) return rc;
+  if (int rc = stem_prepare(gg, current_device_cus(), &g, &lds)) return rc;
   // 16-byte input row and weight loads, 16-byte output stores
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
       (reinterpret_cast<uintptr_t>(y) & 15u))

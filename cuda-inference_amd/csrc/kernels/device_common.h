@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "gie_hip.h"
 
 namespace gie_hip {
@@ -62,5 +64,18 @@ __device__ __forceinline__ uint16_t epilogue(float acc, const uint16_t* __restri
 }
 
 inline int ceil_div_i(long long a, long long b) { return int((a + b - 1) / b); }
+
+// Compute units of the current device, queried once per device and kept (grid sizing on every launch must not
+// pay an attribute query). 256 (MI355X) when the query fails.
+inline int current_device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus > 0) return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  cached[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
 
 }  // namespace gie_hip

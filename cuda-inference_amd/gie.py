@@ -128,6 +128,7 @@ _CAPI = {
     "gie_tune_cache_size": ([_cp, ctypes.POINTER(_sz)], _i),
     "gie_tune_cache_clear": ([_cp], _i),
     "gie_estimate_kernel": ([_cp, _PP, _dp, _ip], _i),
+    "gie_measure_host_cost": ([_PP, ctypes.POINTER(GieOptions), _i, _dp], _i),
     "gie_model_estimate": ([_cp, _PP, ctypes.POINTER(GieDeviceModel), _dp, _ip], _i),
     "gie_model_rank": ([_PP, ctypes.POINTER(GieDeviceModel), ctypes.c_char_p, _sz, _dp, _i, _ip], _i),
     "gie_measure_ceilings": ([_i, _i, _dp, _ip], _i),
@@ -533,6 +534,15 @@ def forward_n(p: Problem, t: ConvTensors, workspace: DeviceBuffer | None, stream
                                       ctypes.byref(b) if b is not None else None, ctypes.byref(y),
                                       workspace.addr if workspace else None, workspace.nbytes if workspace else 0,
                                       stream.h if stream else None, ctypes.byref(oc), count), "Conv2D::forward x n")
+
+
+def measure_host_cost(p: Problem, batch: int = 256, **opt) -> dict:
+    """Host wall time per Conv2D::forward call (plan cached) and per bare kernel launch, plus the GPU time per
+    forward, over batches of `batch` back-to-back calls (the library's own measurement, from C++)."""
+    pc, oc = p.c(), _opts(**opt)
+    out = (ctypes.c_double * 3)()
+    check(capi().gie_measure_host_cost(ctypes.byref(pc), ctypes.byref(oc), batch, out), "measure_host_cost")
+    return {"host_us_per_forward": out[0], "host_us_per_bare_launch": out[1], "device_us_per_forward": out[2]}
 
 
 DISTRIBUTIONS = {"uniform": 0, "normal": 1, "sparse_signed": 2, "positive": 3}

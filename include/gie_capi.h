@@ -55,6 +55,11 @@ int gie_conv2d_forward(const gie_problem* p, const gie_tensor* x, const gie_tens
 int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
                          const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
                          const gie_options* opt, int count);
+/* Host cost of the plan API, no counterpart in the reference: median host wall time to enqueue one
+   gie_conv2d_forward call on problem p (zero-filled tensors, plan already cached) and one bare empty-kernel launch,
+   each over batches of `batch` back-to-back calls; out3 = {host us per forward, host us per bare launch,
+   device us per forward}. */
+int gie_measure_host_cost(const gie_problem* p, const gie_options* opt, int batch, double* out3);
 int gie_conv2d_workspace_size(const gie_problem* p, const gie_options* opt, size_t* bytes);
 int gie_conv2d_clear_plan_cache(void);
 
