@@ -182,6 +182,80 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 // kDma4 = 4-byte direct-to-LDS loads of every padded position; kReg2 = 2-byte register loads (odd rows).
 constexpr int kX16 = 0, kDma4 = 1, kReg2 = 2;
 
+// Epilogue of one unit, shared by the slab kernels: tap-column shifts (DPP), then split 1: bias + ReLU + one rounding
+// and pixel-pair (or 2-byte) stores straight from the accumulators; split > 1: FP32 partials.
+template <typename E, int P, int NBW>
+__device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uint32_t (&bbits)[4], int lane, int wr,
+                                           int oh0, int nrows, int b, int z, int o0, int f0,
+                                           uint16_t* __restrict__ y, float* __restrict__ partial, const SlabGeom& g) {
+  constexpr int RW = 16 * NBW / P;
+  float bv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bv[i] = E::to_f32(uint16_t(bbits[i]));
+  const uint32_t oddm = 0u - uint32_t(lane & 1);  // all ones on odd lanes
+  const bool all_f = o0 + kSlTO <= g.O;            // the whole 32-filter block exists (wave-uniform)
+  const long long fbase = (static_cast<long long>(b) * g.O + f0) * g.HW;
+  // pixel-pair stores: even lane (column c) stores filters 0, 1 at (c, c+1), odd lane filters 2, 3 at (c-1, c)
+  uint16_t* const ypair = y + fbase + (static_cast<long long>(g.HW * 2 - 1) & (long long)(int)oddm);
+  float* const pdst = partial + static_cast<long long>(z) * g.total + fbase;
+  const int f_pair = f0 + int(oddm & 2u);
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
+    if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
+    if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
+    const int p = wr * RW * P + 16 * j + (lane & 15);
+    const int row = p / P, col = p % P;
+    const int pix = (oh0 + row) * g.W + col;
+    const bool valid = col < g.W && row < nrows;
+    if (g.split > 1) {
+      if (valid) {
+        if (all_f) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pdst[pix + i * g.HW] = out[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (f0 + i < g.O) pdst[pix + i * g.HW] = out[i];
+        }
+      }
+      continue;
+    }
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = out[i] + bv[i];
+      if (g.relu) v = fmaxf(v, 0.0f);
+      h[i] = E::from_f32(v);
+    }
+    if (g.y_vec) {
+      const uint32_t lo01 = h[0] | (h[1] << 16), lo23 = h[2] | (h[3] << 16);
+      const uint32_t send = (lo01 & oddm) | (lo23 & ~oddm);
+      const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap lane pairs
+      // even: (h0, recv.lo) and (h1, recv.hi); odd: (recv.lo, h2) and (recv.hi, h3)
+      const uint32_t wa_e = (h[0] & 0xffffu) | (recv << 16), wb_e = (h[1] & 0xffffu) | (recv & 0xffff0000u);
+      const uint32_t wa_o = (recv & 0xffffu) | (h[2] << 16), wb_o = (recv >> 16) | (h[3] << 16);
+      const uint32_t wa = (wa_o & oddm) | (wa_e & ~oddm), wb = (wb_o & oddm) | (wb_e & ~oddm);
+      // the odd lane's pair starts at column c - 1, which is valid when its own column is
+      if (col - int(oddm & 1u) < g.W && row < nrows) {
+        uint32_t* const da = reinterpret_cast<uint32_t*>(ypair + pix);
+        if (all_f || f_pair < g.O) da[0] = wa;
+        if (all_f || f_pair + 1 < g.O) da[g.HW / 2] = wb;
+      }
+    } else if (valid) {
+      uint16_t* const dst = y + fbase + pix;
+      if (all_f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i * g.HW] = uint16_t(h[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (f0 + i < g.O) dst[i * g.HW] = uint16_t(h[i]);
+      }
+    }
+  }
+}
+
 template <typename E, int P, int NBW, int NST, int MODE>
 __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                      const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
@@ -542,83 +616,194 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
   }
 
   // ---- epilogue: tap-column shifts, bias + ReLU + one rounding, stores straight from the registers ----
-  float bv[4];
+  slab_store<E, P, NBW>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
+}
+
+// ---- lean form: two workgroups per CU ----
+// The same units, LDS layout and direct-to-LDS loads as slab_kernel with two load stages (kDma4 form only), held in at
+// most 256 VGPR+AGPR per lane so that two workgroups share each CU and cover each other's waits and barriers:
+//   * one set of weight fragments, rebuilt at the start of each slice from the staged OIHW rows;
+//   * pixel fragments read one tap row at a time: row r reads only the blocks no earlier row needed;
+//   * slice i + 1 loads into the other stage right after the barrier that starts slice i (every wave has finished
+//     slice i - 1 there by then), so each slice's loads overlap one slice of MFMAs.
+template <int P, int NBW>
+struct LeanRows {
+  static constexpr int G = P >= 16 ? 16 : P;
+  static constexpr int first_row(int u) {  // first tap row whose MFMAs read pixel block u
+    for (int r = 0; r < 3; ++r)
+      for (int j = 0; j < NBW; ++j)
+        if ((16 * j + r * P) / G == u) return r;
+    return 3;
+  }
+};
+
+template <typename E, int P, int NBW>
+__global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                          float* __restrict__ partial, SlabGeom g) {
+  using Sh = SlabShape<P, NBW, 2>;
+  using Rows = LeanRows<P, NBW>;
+  constexpr int CS = Sh::CS, NW = Sh::NW, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G, NBR = Sh::NBR;
+  constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
+  constexpr int ACT = Sh::ACT, KA = Sh::KA, R = Sh::R;
+  constexpr int WOFF = 2 * ACT;  // LDS: [2 activation stages][2 weight stages]
+  static_assert(Sh::LDS <= 80 * 1024, "two workgroups per CU");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fh = wave & 1, wr = wave >> 1;
+
+  const int slot = int(blockIdx.x);
+  const int unit = (slot >> 3) + (slot & 7) * g.per_xcd;
+  if (unit >= g.n_units) return;  // workgroup-uniform
+  int rest = unit;
+  const int ob = rest % g.n_ob;
+  rest /= g.n_ob;
+  const int band = rest % g.n_bands;
+  rest /= g.n_bands;
+  const int b = rest % g.B, z = rest / g.B;
+  const int o0 = ob * kSlTO, oh0 = band * RB;
+  const int s_beg = (g.S * z) / g.split, ns = (g.S * (z + 1)) / g.split - s_beg;
+  const int nrows = min(RB, g.H - oh0);
+
+  const v4i xr = make_vsharp(x, g.x_bytes);
+  const v4i wrs = make_vsharp(w, g.w_bytes);
+  const unsigned lds0 = lds_addr(lds);
+
+  const int f0 = o0 + fh * 16 + 4 * (lane >> 4);
+  uint32_t bbits[4] = {0u, 0u, 0u, 0u};
+  if (g.split == 1 && bias != nullptr) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) bv[i] = E::to_f32(uint16_t(bbits[i]));
-  const uint32_t oddm = 0u - uint32_t(lane & 1);  // all ones on odd lanes
-  const bool all_f = o0 + kSlTO <= g.O;            // the whole 32-filter block exists (wave-uniform)
-  const long long fbase = (static_cast<long long>(b) * g.O + f0) * g.HW;
-  // pixel-pair stores: even lane (column c) stores filters 0, 1 at (c, c+1), odd lane filters 2, 3 at (c-1, c)
-  uint16_t* const ypair = y + fbase + (static_cast<long long>(g.HW * 2 - 1) & (long long)(int)oddm);
-  float* const pdst = partial + static_cast<long long>(z) * g.total + fbase;
-  const int f_pair = f0 + int(oddm & 2u);
+    for (int i = 0; i < 4; ++i) bbits[i] = bias[min(f0 + i, g.O - 1)];
+  }
+
+  int w_voff[KBW];
 #pragma unroll
-  for (int j = 0; j < NBW; ++j) {
-    f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
-    if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
-    if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
-    const int p = wr * RW * P + 16 * j + (lane & 15);
-    const int row = p / P, col = p % P;
-    const int pix = (oh0 + row) * g.W + col;
-    const bool valid = col < g.W && row < nrows;
-    if (g.split > 1) {
-      if (valid) {
-        if (all_f) {
+  for (int kb = 0; kb < KBW; ++kb) {
+    const int u = (wave + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
+    w_voff[kb] = (f < kSlTO && k < WCH && o0 + f < g.O) ? (o0 + f) * g.C * 18 + 16 * k : kOut;
+  }
+  int w_soff = s_beg * CS * 18;
+  int w_rem = g.C - s_beg * CS;
+  int a_c0 = s_beg * CS;
+  constexpr int NV = 4 * R;
+  int a_voff[NV];
+  const int a_soff0 = (b * g.C + 8 * wave) * g.HW * 2;
+  {
+    const int swz_hi = (wave & 1) << 2;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) pdst[pix + i * g.HW] = out[i];
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (f0 + i < g.O) pdst[pix + i * g.HW] = out[i];
-        }
-      }
-      continue;
-    }
-    uint32_t h[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = out[i] + bv[i];
-      if (g.relu) v = fmaxf(v, 0.0f);
-      h[i] = E::from_f32(v);
-    }
-    if (g.y_vec) {
-      const uint32_t lo01 = h[0] | (h[1] << 16), lo23 = h[2] | (h[3] << 16);
-      const uint32_t send = (lo01 & oddm) | (lo23 & ~oddm);
-      const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap lane pairs
-      // even: (h0, recv.lo) and (h1, recv.hi); odd: (recv.lo, h2) and (recv.hi, h3)
-      const uint32_t wa_e = (h[0] & 0xffffu) | (recv << 16), wb_e = (h[1] & 0xffffu) | (recv & 0xffff0000u);
-      const uint32_t wa_o = (recv & 0xffffu) | (h[2] << 16), wb_o = (recv >> 16) | (h[3] << 16);
-      const uint32_t wa = (wa_o & oddm) | (wa_e & ~oddm), wb = (wb_o & oddm) | (wb_e & ~oddm);
-      // the odd lane's pair starts at column c - 1, which is valid when its own column is
-      if (col - int(oddm & 1u) < g.W && row < nrows) {
-        uint32_t* const da = reinterpret_cast<uint32_t*>(ypair + pix);
-        if (all_f || f_pair < g.O) da[0] = wa;
-        if (all_f || f_pair + 1 < g.O) da[g.HW / 2] = wb;
-      }
-    } else if (valid) {
-      uint16_t* const dst = y + fbase + pix;
-      if (all_f) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i * g.HW] = uint16_t(h[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (f0 + i < g.O) dst[i * g.HW] = uint16_t(h[i]);
-      }
+    for (int v = 0; v < NV; ++v) {
+      const int seg = (v % R) * 8 + (lane >> 3);
+      const int pos = ((seg ^ ((v / R) | swz_hi)) << 4) + 2 * (lane & 7);
+      const int row = pos / P, col = pos % P, ih = oh0 - 1 + row;
+      a_voff[v] = (row < NR && ih >= 0 && ih < g.H && col < g.W) ? (ih * g.W + col) * 2 : kOut;
     }
   }
+  auto issue = [&](int st) __attribute__((always_inline)) {  // the next slice in order into stage st
+    const unsigned ab = lds0 + unsigned(st * ACT + wave * KA * 256);
+#pragma unroll
+    for (int i = 0; i < KA; ++i) {
+      const int soff = a_soff0 + (a_c0 + i / R) * g.HW * 2;
+      dma4s(xr, ab + unsigned(i * 256), a_c0 + 8 * wave + i / R < g.C ? a_voff[(i % R) + R * ((i / R) & 3)] : kOut,
+            soff);
+    }
+    a_c0 += CS;
+    const unsigned wb = lds0 + unsigned(WOFF + st * WST);
+    if (w_rem >= CS) {
+#pragma unroll
+      for (int kb = 0; kb < KBW; ++kb) dma16s(wrs, wb + unsigned((wave + NW * kb) * 1024), w_voff[kb], w_soff);
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KBW; ++kb) {
+        const int u = (wave + NW * kb) * 64 + lane, k = u - (u / CPF) * CPF;
+        dma16s(wrs, wb + unsigned((wave + NW * kb) * 1024), 8 * k < 9 * w_rem ? w_voff[kb] : kOut, w_soff);
+      }
+    }
+    w_soff += CS * 18;
+    w_rem -= CS;
+  };
+
+  const unsigned a_rd = lds0 + unsigned(WOFF + (fh * 16 + (lane & 15)) * WPITCH + 8 * (lane >> 4) * 18);
+  unsigned b_rd[NBR][2];
+#pragma unroll
+  for (int u = 0; u < NBR; ++u) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ch = 8 * (lane >> 4) + 4 * h + ((lane & 15) >> 2);
+      const int pos = wr * RW * P + u * G + 4 * (lane & 3);
+      b_rd[u][h] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
+    }
+  }
+
+  f32x4 acc[3][NBW];
+#pragma unroll
+  for (int s2 = 0; s2 < 3; ++s2) {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[s2][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  u32x4 fw[9], fb[NBR];
+  uint32_t d[36];
+
+  auto slice = [&](int i, auto st_c) __attribute__((always_inline)) {
+    constexpr int st = decltype(st_c)::value;
+    wait_vmcnt<0>();  // this wave's loads of slice i (the only ones in flight)
+    stage_barrier();  // every wave's loads of slice i have landed and every wave has finished slice i - 1
+    if (i + 1 < ns) issue(st ^ 1);
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const u32x4 v = rd16(a_rd + unsigned(st * WST + 16 * t));
+      d[4 * t] = v.x, d[4 * t + 1] = v.y, d[4 * t + 2] = v.z, d[4 * t + 3] = v.w;
+    }
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+      for (int u = 0; u < NBR; ++u) {
+        if (Rows::first_row(u) == r) {
+          const u32x2 lo = rd_tr(b_rd[u][0] + unsigned(st * ACT)), hi = rd_tr(b_rd[u][1] + unsigned(st * ACT));
+          fb[u] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+      }
+#pragma unroll
+      for (int sc = 0; sc < 3; ++sc) {
+        const int t = 3 * r + sc;
+        if (r == 0) fw[t] = u32x4{pick2(d, t, 9 + t), pick2(d, 18 + t, 27 + t), pick2(d, 36 + t, 45 + t),
+                                  pick2(d, 54 + t, 63 + t)};
+        if (r == 0 && sc == 2) {
+#pragma unroll
+          for (int t2 = 3; t2 < 9; ++t2)
+            fw[t2] = u32x4{pick2(d, t2, 9 + t2), pick2(d, 18 + t2, 27 + t2), pick2(d, 36 + t2, 45 + t2),
+                           pick2(d, 54 + t2, 63 + t2)};
+        }
+#pragma unroll
+        for (int j = 0; j < NBW; ++j) acc[sc][j] = E::mfma(fw[t], fb[(16 * j + r * P) / G], acc[sc][j]);
+      }
+    }
+  };
+
+  if (ns > 0) issue(0);
+  for (int i = 0; i < ns; i += 2) {
+    slice(i, std::integral_constant<int, 0>{});
+    if (i + 1 < ns) slice(i + 1, std::integral_constant<int, 1>{});
+  }
+  slab_store<E, P, NBW>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
 }
 
 struct SlabCfg {
   int P, NBW, NST;
+  bool lean;  // slab_lean_kernel: two stages, two workgroups per CU
 };
-// (row pitch, 16-position blocks per wave, load stages)
-constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3}, {16, 7, 2}, {16, 4, 3}, {8, 2, 3}, {8, 4, 3}, {32, 4, 3}};
+// (row pitch, 16-position blocks per wave, load stages, lean form)
+constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3, false}, {16, 7, 2, false}, {16, 4, 3, false}, {8, 2, 3, false},
+                                 {8, 4, 3, false},  {32, 4, 3, false}, {16, 7, 2, true},  {16, 4, 2, true},
+                                 {8, 2, 2, true},   {8, 4, 2, true},   {32, 4, 2, true}};
 constexpr int kSlabN = int(sizeof(kSlabCfgs) / sizeof(kSlabCfgs[0]));
 
 template <int I>
 struct CfgT {
   static constexpr int P = kSlabCfgs[I].P, NBW = kSlabCfgs[I].NBW, NST = kSlabCfgs[I].NST;
+  static constexpr bool LEAN = kSlabCfgs[I].lean;
   using Sh = SlabShape<P, NBW, NST>;
 };
 
@@ -629,6 +814,11 @@ typedef void (*SlabFn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16
 template <int I>
 SlabFn pick_fn(bool bf, int mode) {
   using C = CfgT<I>;
+  if constexpr (C::LEAN) {
+    static_assert(C::NST == 2, "the lean form has two stages");
+    if (mode == kDma4) return bf ? &slab_lean_kernel<Bf16, C::P, C::NBW> : &slab_lean_kernel<Fp16, C::P, C::NBW>;
+    return nullptr;
+  }
   if (mode == kDma4)
     return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kDma4> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kDma4>;
   if constexpr (C::NST >= 3) {
@@ -816,9 +1006,10 @@ extern "C" int gie_hip_slab_config_get(int index, gie_slab_config* out) {
   out->pitch = c.P;
   out->tile_k = 32;
   out->stages = c.NST;
+  out->workgroups_per_cu = c.lean ? 2 : 1;
   out->threads = sp.nt;
   out->lds_bytes = sp.lds;
-  out->version = 3;
+  out->version = 4;
   return GIE_HIP_OK;
 }
 

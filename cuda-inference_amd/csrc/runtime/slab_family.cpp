@@ -113,8 +113,8 @@ struct Fns {
   static double extra_traffic(const ConvProblem& prob) {  // FP32 partials written and read back
     return e().split > 1 ? 2.0 * e().split * double(prob.p.output_shape().numel()) * 4.0 : 0.0;
   }
-  // 256 threads holding ~400 VGPR+AGPR each: one workgroup per CU whatever the LDS
-  static int occupancy(const ConvProblem&) { return 1; }
+  // the full form holds ~400 VGPR+AGPR per lane (one workgroup per CU); the lean form 256 at most (two)
+  static int occupancy(const ConvProblem&) { return e().info.workgroups_per_cu; }
   // Useful output positions per step-equivalent: every slab of rows runs the step sequence of the widest
   // configuration (224 positions x 32 filters), whatever its own rows x pitch, because a step's time is set by its
   // loads and waits more than by its MFMA count; times the filter and channel padding.
@@ -155,7 +155,7 @@ struct Fns {
   }
 };
 
-constexpr int kMaxEntries = 64;
+constexpr int kMaxEntries = 96;
 
 template <int I>
 void fill_fns(int idx, KernelDesc& k) {
@@ -194,11 +194,14 @@ void register_slab_family(std::vector<KernelDesc>& out) {
     KernelDesc k;
     k.name = std::string("slab_") + to_string(en.precision) + "_3x3_" + std::to_string(en.info.tile_m) + "x" +
              std::to_string(en.info.rows) + "r" + std::to_string(en.info.pitch) + "_k" +
-             std::to_string(en.info.tile_k) + "_s" + std::to_string(en.info.stages) + "_sk" + std::to_string(en.split);
+             std::to_string(en.info.tile_k) + "_s" + std::to_string(en.info.stages) +
+             (en.info.workgroups_per_cu > 1 ? "_o" + std::to_string(en.info.workgroups_per_cu) : std::string()) + "_sk" +
+             std::to_string(en.split);
     k.backend = Backend::kTensorCore;
     k.version = en.info.version;
     k.params = {{"block_m", en.info.tile_m}, {"rows", en.info.rows}, {"pitch", en.info.pitch},
                 {"block_k", en.info.tile_k}, {"kernel_h", 3}, {"kernel_w", 3}, {"stages", en.info.stages},
+                {"workgroups_per_cu", en.info.workgroups_per_cu},
                 {"split_k", en.split}};
     k.threads_per_block = en.info.threads;
     k.tile_m = en.info.tile_m;

@@ -217,10 +217,12 @@ int gie_hip_conv_narrow(int dtype, const gie_conv_geom* g, const void* x, const 
                         void* stream);
 
 /* One registered slab configuration: tile_m (32) output channels x a slab of `rows` output rows of one image laid
-   out `pitch` positions per row (in_w + 1 <= pitch), channel slices of tile_k, `stages` LDS load stages. */
+   out `pitch` positions per row (in_w + 1 <= pitch), channel slices of tile_k, `stages` LDS load stages,
+   `workgroups_per_cu` resident workgroups per compute unit. */
 typedef struct gie_slab_config {
   int tile_m, rows, pitch, tile_k;
   int stages;
+  int workgroups_per_cu; /* 2: the lean form (at most 80 KiB LDS, 256 VGPR+AGPR per lane) */
   int threads;
   int lds_bytes;
   int version;
