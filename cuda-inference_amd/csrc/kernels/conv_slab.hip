@@ -56,7 +56,13 @@ struct SlabGeom {
   int y_vec;                   // outputs leave as 4-byte pixel pairs
   long long total;             // |Y| elements (partial stride)
   float inv_hw, inv_w;         // 1 / HW, 1 / W for fdiv
+  unsigned mg_ob, mg_band, mg_b;  // n / d = (umulhi(n, mg) + n) >> sh for d = n_ob, n_bands, B (n < 2^30)
+  int sh_ob, sh_band, sh_b;
 };
+
+__device__ __forceinline__ int magic_div(int n, unsigned mg, int sh) {
+  return int((__umulhi(unsigned(n), mg) + unsigned(n)) >> sh);
+}
 
 template <int P, int NBW, int NST>
 struct SlabShape {
@@ -182,53 +188,66 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 // kDma4 = 4-byte direct-to-LDS loads of every padded position; kReg2 = 2-byte register loads (odd rows).
 constexpr int kX16 = 0, kDma4 = 1, kReg2 = 2;
 
+// 4- and 2-byte buffer stores whose out-of-range offsets (kOut) the hardware drops: the epilogue masks lanes and
+// filters through the offset instead of the execution mask
+__device__ __forceinline__ void store4(v4i rsrc, int voff, uint32_t v) {
+  asm volatile("buffer_store_dword %0, %1, %2, 0 offen" ::"v"(v), "v"(voff), "s"(uniform4(rsrc)) : "memory");
+}
+__device__ __forceinline__ void store2(v4i rsrc, int voff, uint32_t v) {
+  asm volatile("buffer_store_short %0, %1, %2, 0 offen" ::"v"(v), "v"(voff), "s"(uniform4(rsrc)) : "memory");
+}
+
 // Epilogue of one unit, shared by the slab kernels: tap-column shifts (DPP), then split 1: bias + ReLU + one rounding
-// and pixel-pair (or 2-byte) stores straight from the accumulators; split > 1: FP32 partials.
+// and pixel-pair (or 2-byte) stores straight from the accumulators; split > 1: FP32 partials. One loop per store
+// form; positions outside the image and filters past O store to kOut (dropped), so no lane is masked by branches.
 template <typename E, int P, int NBW>
 __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uint32_t (&bbits)[4], int lane, int wr,
                                            int oh0, int nrows, int b, int z, int o0, int f0,
                                            uint16_t* __restrict__ y, float* __restrict__ partial, const SlabGeom& g) {
   constexpr int RW = 16 * NBW / P;
-  float bv[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) bv[i] = E::to_f32(uint16_t(bbits[i]));
-  const uint32_t oddm = 0u - uint32_t(lane & 1);  // all ones on odd lanes
-  const bool all_f = o0 + kSlTO <= g.O;            // the whole 32-filter block exists (wave-uniform)
-  const long long fbase = (static_cast<long long>(b) * g.O + f0) * g.HW;
-  // pixel-pair stores: even lane (column c) stores filters 0, 1 at (c, c+1), odd lane filters 2, 3 at (c-1, c)
-  uint16_t* const ypair = y + fbase + (static_cast<long long>(g.HW * 2 - 1) & (long long)(int)oddm);
-  float* const pdst = partial + static_cast<long long>(z) * g.total + fbase;
-  const int f_pair = f0 + int(oddm & 2u);
-#pragma unroll
-  for (int j = 0; j < NBW; ++j) {
+  (void)o0;
+  auto column = [&](int j) __attribute__((always_inline)) {
     f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
     if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
     if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
-    const int p = wr * RW * P + 16 * j + (lane & 15);
-    const int row = p / P, col = p % P;
-    const int pix = (oh0 + row) * g.W + col;
-    const bool valid = col < g.W && row < nrows;
-    if (g.split > 1) {
-      if (valid) {
-        if (all_f) {
+    return out;
+  };
+  const int nf = g.O - f0;                         // filters of the lane's four that exist (>= 4: all)
+  const int fbase = (b * g.O + f0) * g.HW;         // element index of (b, f0, 0)
+  if (g.split > 1) {
+    const v4i pr = make_vsharp(partial + static_cast<long long>(z) * g.total, int(g.total * 4));
 #pragma unroll
-          for (int i = 0; i < 4; ++i) pdst[pix + i * g.HW] = out[i];
-        } else {
+    for (int j = 0; j < NBW; ++j) {
+      const f32x4 out = column(j);
+      const int p = wr * RW * P + 16 * j + (lane & 15), row = p / P, col = p % P;
+      const bool valid = col < g.W && row < nrows;
+      const int e = fbase + (oh0 + row) * g.W + col;
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (f0 + i < g.O) pdst[pix + i * g.HW] = out[i];
-        }
-      }
-      continue;
+      for (int i = 0; i < 4; ++i)
+        store4(pr, valid && i < nf ? (e + i * g.HW) * 4 : kOut, __float_as_uint(out[i]));
     }
-    uint32_t h[4];
+    return;
+  }
+  float bv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bv[i] = E::to_f32(uint16_t(bbits[i]));
+  const v4i yr = make_vsharp(y, int(g.total * 2));
+  auto finish = [&](const f32x4& out, uint32_t (&h)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v = out[i] + bv[i];
-      if (g.relu) v = fmaxf(v, 0.0f);
-      h[i] = E::from_f32(v);
+      const float v = out[i] + bv[i];
+      h[i] = E::from_f32(g.relu ? fmaxf(v, 0.0f) : v);
     }
-    if (g.y_vec) {
+  };
+  if (g.y_vec) {
+    // pixel pairs: even lane (column c) stores filters 0, 1 at (c, c+1), odd lane filters 2, 3 at (c-1, c)
+    const uint32_t oddm = 0u - uint32_t(lane & 1);  // all ones on odd lanes
+    const int fp = int(oddm & 2u);                   // first filter of the lane's pair stores
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      uint32_t h[4];
+      finish(column(j), h);
+      const int p = wr * RW * P + 16 * j + (lane & 15), row = p / P, col = p % P;
       const uint32_t lo01 = h[0] | (h[1] << 16), lo23 = h[2] | (h[3] << 16);
       const uint32_t send = (lo01 & oddm) | (lo23 & ~oddm);
       const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap lane pairs
@@ -237,22 +256,22 @@ __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uin
       const uint32_t wa_o = (recv & 0xffffu) | (h[2] << 16), wb_o = (recv >> 16) | (h[3] << 16);
       const uint32_t wa = (wa_o & oddm) | (wa_e & ~oddm), wb = (wb_o & oddm) | (wb_e & ~oddm);
       // the odd lane's pair starts at column c - 1, which is valid when its own column is
-      if (col - int(oddm & 1u) < g.W && row < nrows) {
-        uint32_t* const da = reinterpret_cast<uint32_t*>(ypair + pix);
-        if (all_f || f_pair < g.O) da[0] = wa;
-        if (all_f || f_pair + 1 < g.O) da[g.HW / 2] = wb;
-      }
-    } else if (valid) {
-      uint16_t* const dst = y + fbase + pix;
-      if (all_f) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i * g.HW] = uint16_t(h[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (f0 + i < g.O) dst[i * g.HW] = uint16_t(h[i]);
-      }
+      const bool pv = col - int(oddm & 1u) < g.W && row < nrows;
+      const int e = fbase + fp * g.HW + (oh0 + row) * g.W + col - int(oddm & 1u);
+      store4(yr, pv && fp < nf ? e * 2 : kOut, wa);
+      store4(yr, pv && fp + 1 < nf ? (e + g.HW) * 2 : kOut, wb);
     }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    uint32_t h[4];
+    finish(column(j), h);
+    const int p = wr * RW * P + 16 * j + (lane & 15), row = p / P, col = p % P;
+    const bool valid = col < g.W && row < nrows;
+    const int e = fbase + (oh0 + row) * g.W + col;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store2(yr, valid && i < nf ? (e + i * g.HW) * 2 : kOut, h[i]);
   }
 }
 
@@ -637,60 +656,63 @@ struct LeanRows {
   }
 };
 
-template <typename E, int P, int NBW>
+template <typename E, int P, int NBW, int NST>
 __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
                                                           const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
                                                           float* __restrict__ partial, SlabGeom g) {
-  using Sh = SlabShape<P, NBW, 2>;
+  using Sh = SlabShape<P, NBW, NST>;
   using Rows = LeanRows<P, NBW>;
   constexpr int CS = Sh::CS, NW = Sh::NW, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G, NBR = Sh::NBR;
   constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
   constexpr int ACT = Sh::ACT, KA = Sh::KA, R = Sh::R;
-  constexpr int WOFF = 2 * ACT;  // LDS: [2 activation stages][2 weight stages]
-  static_assert(Sh::LDS <= 80 * 1024, "two workgroups per CU");
+  constexpr int WOFF = NST * ACT;  // LDS: [NST activation stages][NST weight stages]
+  constexpr int NI = KBW + KA;     // loads per wave per slice
+  static_assert(NST > 2 || Sh::LDS <= 80 * 1024, "two stages: two workgroups per CU");
+  static_assert((NST - 1) * NI < 64, "loads in flight fit the vmcnt counter");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fh = wave & 1, wr = wave >> 1;
 
+  // ---- unit (all wave-uniform): divisions by host-computed magic numbers ----
   const int slot = int(blockIdx.x);
   const int unit = (slot >> 3) + (slot & 7) * g.per_xcd;
-  if (unit >= g.n_units) return;  // workgroup-uniform
-  int rest = unit;
-  const int ob = rest % g.n_ob;
-  rest /= g.n_ob;
-  const int band = rest % g.n_bands;
-  rest /= g.n_bands;
-  const int b = rest % g.B, z = rest / g.B;
+  if (unit >= g.n_units) return;
+  const int q_ob = magic_div(unit, g.mg_ob, g.sh_ob), ob = unit - q_ob * g.n_ob;
+  const int q_band = magic_div(q_ob, g.mg_band, g.sh_band), band = q_ob - q_band * g.n_bands;
+  const int z = magic_div(q_band, g.mg_b, g.sh_b), b = q_band - z * g.B;
   const int o0 = ob * kSlTO, oh0 = band * RB;
-  const int s_beg = (g.S * z) / g.split, ns = (g.S * (z + 1)) / g.split - s_beg;
+  int s_beg = 0, ns = g.S;
+  if (g.split > 1) {
+    s_beg = (g.S * z) / g.split;
+    ns = (g.S * (z + 1)) / g.split - s_beg;
+  }
   const int nrows = min(RB, g.H - oh0);
 
   const v4i xr = make_vsharp(x, g.x_bytes);
   const v4i wrs = make_vsharp(w, g.w_bytes);
   const unsigned lds0 = lds_addr(lds);
 
+  // bias of the lane's four filters by counted loads: issued first, so the first slice's wait covers them
   const int f0 = o0 + fh * 16 + 4 * (lane >> 4);
-  uint32_t bbits[4] = {0u, 0u, 0u, 0u};
-  if (g.split == 1 && bias != nullptr) {
+  uint32_t bbits[4];
+  {
+    const v4i br = make_vsharp(bias, g.split == 1 && bias != nullptr ? 2 * g.O : 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bbits[i] = bias[min(f0 + i, g.O - 1)];
+    for (int i = 0; i < 4; ++i) bbits[i] = load2s(br, 2 * min(f0 + i, g.O - 1), 0);
   }
 
+  // ---- direct-load offsets: per lane fixed across slices; per slice only the scalar offsets move ----
   int w_voff[KBW];
 #pragma unroll
   for (int kb = 0; kb < KBW; ++kb) {
     const int u = (wave + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
     w_voff[kb] = (f < kSlTO && k < WCH && o0 + f < g.O) ? (o0 + f) * g.C * 18 + 16 * k : kOut;
   }
-  int w_soff = s_beg * CS * 18;
-  int w_rem = g.C - s_beg * CS;
-  int a_c0 = s_beg * CS;
   constexpr int NV = 4 * R;
   int a_voff[NV];
-  const int a_soff0 = (b * g.C + 8 * wave) * g.HW * 2;
   {
     const int swz_hi = (wave & 1) << 2;
 #pragma unroll
@@ -701,29 +723,38 @@ __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __res
       a_voff[v] = (row < NR && ih >= 0 && ih < g.H && col < g.W) ? (ih * g.W + col) * 2 : kOut;
     }
   }
-  auto issue = [&](int st) __attribute__((always_inline)) {  // the next slice in order into stage st
+  const int hw2 = g.HW * 2;
+  int c_next = s_beg * CS;  // first channel of the next slice to load (wave-uniform)
+  // the next slice into stage st: this wave's 8 channels' padded planes (KA 4-byte loads) and its share of the
+  // 32 filters' OIHW runs (KBW 16-byte loads); channels past C load zeros
+  auto issue = [&](int st) __attribute__((always_inline)) {
     const unsigned ab = lds0 + unsigned(st * ACT + wave * KA * 256);
-#pragma unroll
-    for (int i = 0; i < KA; ++i) {
-      const int soff = a_soff0 + (a_c0 + i / R) * g.HW * 2;
-      dma4s(xr, ab + unsigned(i * 256), a_c0 + 8 * wave + i / R < g.C ? a_voff[(i % R) + R * ((i / R) & 3)] : kOut,
-            soff);
-    }
-    a_c0 += CS;
     const unsigned wb = lds0 + unsigned(WOFF + st * WST);
-    if (w_rem >= CS) {
+    const int a_soff = (b * g.C + c_next + 8 * wave) * hw2;
+    const int w_soff = c_next * 18;
+    if (c_next + CS <= g.C) {
+#pragma unroll
+      for (int i = 0; i < KA; ++i)
+        dma4s(xr, ab + unsigned(i * 256), a_voff[(i % R) + R * ((i / R) & 3)], a_soff + (i / R) * hw2);
 #pragma unroll
       for (int kb = 0; kb < KBW; ++kb) dma16s(wrs, wb + unsigned((wave + NW * kb) * 1024), w_voff[kb], w_soff);
     } else {
+      const int w_rem = g.C - c_next;
+#pragma unroll
+      for (int i = 0; i < KA; ++i)
+        dma4s(xr, ab + unsigned(i * 256), c_next + 8 * wave + i / R < g.C ? a_voff[(i % R) + R * ((i / R) & 3)] : kOut,
+              a_soff + (i / R) * hw2);
 #pragma unroll
       for (int kb = 0; kb < KBW; ++kb) {
         const int u = (wave + NW * kb) * 64 + lane, k = u - (u / CPF) * CPF;
         dma16s(wrs, wb + unsigned((wave + NW * kb) * 1024), 8 * k < 9 * w_rem ? w_voff[kb] : kOut, w_soff);
       }
     }
-    w_soff += CS * 18;
-    w_rem -= CS;
+    c_next += CS;
   };
+#pragma unroll
+  for (int st = 0; st + 1 < NST; ++st)
+    if (st < ns) issue(st);
 
   const unsigned a_rd = lds0 + unsigned(WOFF + (fh * 16 + (lane & 15)) * WPITCH + 8 * (lane >> 4) * 18);
   unsigned b_rd[NBR][2];
@@ -741,16 +772,23 @@ __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __res
 #pragma unroll
   for (int s2 = 0; s2 < 3; ++s2) {
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) acc[s2][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j2 = 0; j2 < NBW; ++j2) acc[s2][j2] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   u32x4 fw[9], fb[NBR];
   uint32_t d[36];
 
+  // slice i from stage st = i % NST: all of its LDS reads are requested right after the barrier; slice i + NST - 1's
+  // loads go out (into the stage slice i - 1 used) once the first tap row's MFMAs are issued
   auto slice = [&](int i, auto st_c) __attribute__((always_inline)) {
     constexpr int st = decltype(st_c)::value;
-    wait_vmcnt<0>();  // this wave's loads of slice i (the only ones in flight)
+    // this wave's loads of slice i have landed (slices i + 1 .. i + NST - 2 may still be in flight)
+    if constexpr (NST == 2) {
+      wait_vmcnt<0>();
+    } else {
+      if (i + NST - 2 < ns) wait_vmcnt<(NST - 2) * NI>();
+      else wait_vm_upto<(NST - 2) * NI>((ns - 1 - i) * NI);
+    }
     stage_barrier();  // every wave's loads of slice i have landed and every wave has finished slice i - 1
-    if (i + 1 < ns) issue(st ^ 1);
 #pragma unroll
     for (int t = 0; t < 9; ++t) {
       const u32x4 v = rd16(a_rd + unsigned(st * WST + 16 * t));
@@ -765,28 +803,38 @@ __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __res
           fb[u] = u32x4{lo.x, lo.y, hi.x, hi.y};
         }
       }
+      if (r == 0) {
+#pragma unroll
+        for (int t = 0; t < 9; ++t)
+          fw[t] = u32x4{pick2(d, t, 9 + t), pick2(d, 18 + t, 27 + t), pick2(d, 36 + t, 45 + t), pick2(d, 54 + t, 63 + t)};
+      }
 #pragma unroll
       for (int sc = 0; sc < 3; ++sc) {
         const int t = 3 * r + sc;
-        if (r == 0) fw[t] = u32x4{pick2(d, t, 9 + t), pick2(d, 18 + t, 27 + t), pick2(d, 36 + t, 45 + t),
-                                  pick2(d, 54 + t, 63 + t)};
-        if (r == 0 && sc == 2) {
-#pragma unroll
-          for (int t2 = 3; t2 < 9; ++t2)
-            fw[t2] = u32x4{pick2(d, t2, 9 + t2), pick2(d, 18 + t2, 27 + t2), pick2(d, 36 + t2, 45 + t2),
-                           pick2(d, 54 + t2, 63 + t2)};
-        }
 #pragma unroll
         for (int j = 0; j < NBW; ++j) acc[sc][j] = E::mfma(fw[t], fb[(16 * j + r * P) / G], acc[sc][j]);
+      }
+      if (r == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + NST - 1 < ns) issue((st + NST - 1) % NST);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
 
-  if (ns > 0) issue(0);
-  for (int i = 0; i < ns; i += 2) {
+  for (int i = 0; i < ns; i += NST) {
     slice(i, std::integral_constant<int, 0>{});
-    if (i + 1 < ns) slice(i + 1, std::integral_constant<int, 1>{});
+    if (i + 1 < ns) slice(i + 1, std::integral_constant<int, 1 % NST>{});
+    if constexpr (NST > 2) {
+      if (i + 2 < ns) slice(i + 2, std::integral_constant<int, 2 % NST>{});
+    }
+    if constexpr (NST > 3) {
+      if (i + 3 < ns) slice(i + 3, std::integral_constant<int, 3 % NST>{});
+    }
   }
+  wait_vmcnt<0>();  // the bias loads (already covered by the first slice's wait; stated for the epilogue)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) touch_v(bbits[i]);
   slab_store<E, P, NBW>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
 }
 
@@ -797,7 +845,7 @@ struct SlabCfg {
 // (row pitch, 16-position blocks per wave, load stages, lean form)
 constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3, false}, {16, 7, 2, false}, {16, 4, 3, false}, {8, 2, 3, false},
                                  {8, 4, 3, false},  {32, 4, 3, false}, {16, 7, 2, true},  {16, 4, 2, true},
-                                 {8, 2, 2, true},   {8, 4, 2, true},   {32, 4, 2, true}};
+                                 {8, 2, 2, true},   {8, 4, 2, true},   {32, 4, 2, true},  {16, 7, 3, true}};
 constexpr int kSlabN = int(sizeof(kSlabCfgs) / sizeof(kSlabCfgs[0]));
 
 template <int I>
@@ -815,19 +863,18 @@ template <int I>
 SlabFn pick_fn(bool bf, int mode) {
   using C = CfgT<I>;
   if constexpr (C::LEAN) {
-    static_assert(C::NST == 2, "the lean form has two stages");
-    if (mode == kDma4) return bf ? &slab_lean_kernel<Bf16, C::P, C::NBW> : &slab_lean_kernel<Fp16, C::P, C::NBW>;
+    if (mode == kDma4)
+      return bf ? &slab_lean_kernel<Bf16, C::P, C::NBW, C::NST> : &slab_lean_kernel<Fp16, C::P, C::NBW, C::NST>;
+    return nullptr;
+  } else {
+    if (mode == kDma4)
+      return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kDma4> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kDma4>;
+    if constexpr (C::NST >= 3) {
+      if constexpr (C::Sh::KR <= 16)
+        return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kReg2> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kReg2>;
+    }
     return nullptr;
   }
-  if (mode == kDma4)
-    return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kDma4> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kDma4>;
-  if constexpr (C::NST >= 3) {
-    if (mode == kX16)
-      return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kX16> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kX16>;
-    if constexpr (C::Sh::KR <= 16)
-      return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kReg2> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kReg2>;
-  }
-  return nullptr;
 }
 
 struct SlabShapeInfo {
@@ -873,12 +920,10 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   const int bands = (gg->in_h + si.RB - 1) / si.RB;
   // activation load form: even rows take 4-byte loads (16-byte register loads when the slab is the whole image and
   // x is 16-byte aligned); odd rows or a 2-byte aligned x take 2-byte loads
+  // (the 16-byte register form of whole-image slabs measured slower than the direct loads on config 2: 16.0 vs
+  // 14.9 us, so even rows always take the direct form)
   const bool even = gg->in_w % 2 == 0 && !(reinterpret_cast<uintptr_t>(x) & 3u);
   SlabFn alt = nullptr;
-  if (even && bands == 1 && !(reinterpret_cast<uintptr_t>(x) & 15u)) {
-    dispatch(cfg, bf, kX16, &alt, &si, std::make_integer_sequence<int, kSlabN>{});
-    if (alt != nullptr) fn = alt;  // configurations without the register forms keep the direct loads
-  }
   if (!even) {
     dispatch(cfg, bf, kReg2, &alt, &si, std::make_integer_sequence<int, kSlabN>{});
     fn = alt;
@@ -887,7 +932,8 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   const long long xb = 2LL * gg->batch * gg->in_channels * hw;
   const long long wb = 18LL * gg->out_channels * gg->in_channels;
   const long long total = 1LL * gg->batch * gg->out_channels * hw;
-  if (xb >= (1LL << 30) || wb >= (1LL << 30) || total >= (1LL << 31)) return GIE_HIP_EUNSUPPORTED;
+  // 32-bit buffer offsets with kOut (2^31) past every range: y bytes and FP32 partial bytes below 2^31
+  if (xb >= (1LL << 30) || wb >= (1LL << 30) || total >= (1LL << 29)) return GIE_HIP_EUNSUPPORTED;
   const int S = (gg->in_channels + si.CS - 1) / si.CS;
   if (split < 1 || split > S) return GIE_HIP_EINVAL;
   SlabGeom& g = sp->g;
@@ -899,6 +945,16 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   if (units > (1LL << 30)) return GIE_HIP_EUNSUPPORTED;
   g.n_units = int(units);
   g.per_xcd = (g.n_units + 7) / 8;
+  // n / d for n < 2^30: l = ceil(log2 d), mg = floor(2^32 (2^l - d) / d) + 1, q = (umulhi(n, mg) + n) >> l
+  const auto magic = [](int d, unsigned* mg, int* sh) {
+    int l = 0;
+    while ((1LL << l) < d) ++l;
+    *sh = l;
+    *mg = unsigned((((1ULL << l) - unsigned(d)) << 32) / unsigned(d) + 1);
+  };
+  magic(g.n_ob, &g.mg_ob, &g.sh_ob);
+  magic(g.n_bands, &g.mg_band, &g.sh_band);
+  magic(g.B, &g.mg_b, &g.sh_b);
   g.x_bytes = int(xb), g.w_bytes = int(wb);
   g.relu = gg->relu;
   g.split = split;
@@ -1006,7 +1062,8 @@ extern "C" int gie_hip_slab_config_get(int index, gie_slab_config* out) {
   out->pitch = c.P;
   out->tile_k = 32;
   out->stages = c.NST;
-  out->workgroups_per_cu = c.lean ? 2 : 1;
+  out->workgroups_per_cu = c.lean && sp.lds <= 80 * 1024 ? 2 : 1;
+  out->lean = c.lean ? 1 : 0;
   out->threads = sp.nt;
   out->lds_bytes = sp.lds;
   out->version = 4;

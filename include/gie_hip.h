@@ -222,7 +222,8 @@ int gie_hip_conv_narrow(int dtype, const gie_conv_geom* g, const void* x, const 
 typedef struct gie_slab_config {
   int tile_m, rows, pitch, tile_k;
   int stages;
-  int workgroups_per_cu; /* 2: the lean form (at most 80 KiB LDS, 256 VGPR+AGPR per lane) */
+  int workgroups_per_cu; /* resident workgroups per CU: 2 for the lean form with at most 80 KiB LDS */
+  int lean;              /* 1: the lean form (at most 256 VGPR+AGPR per lane, single-buffered fragments) */
   int threads;
   int lds_bytes;
   int version;

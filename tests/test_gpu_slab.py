@@ -4,8 +4,8 @@ reference's tolerance (tests/conv_test_common.h:83-127) and, at BASELINE sizes, 
 
 Cases cover every registered configuration on slabs that are whole images and images cut into several slabs,
 rows narrower than the pitch, channel counts that are not a multiple of the slice (zero-filled channels), filter
-counts past and below a 32-filter block, each activation load form (16-byte register loads of a whole image,
-4-byte direct-to-LDS loads of several slabs or a 4-byte aligned x, 2-byte loads of odd rows or a 2-byte aligned x),
+counts past and below a 32-filter block, each activation load form (4-byte direct-to-LDS loads of even rows of a
+4-byte aligned x, 2-byte loads of odd rows or a 2-byte aligned x),
 pixel-pair and 2-byte output stores, no bias / no ReLU, both precisions, split-K with the reduce kernel, a second launch giving the
 same bits, and argument rejection.
 """
