@@ -838,21 +838,25 @@ __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __res
   slab_store<E, P, NBW>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
 }
 
+// kernel forms: slab_kernel (double-buffered fragments), slab_lean_kernel (single fragment set, at most 256
+// VGPR+AGPR)
+constexpr int kFull = 0, kLean = 1;
 struct SlabCfg {
   int P, NBW, NST;
-  bool lean;  // slab_lean_kernel: two stages, two workgroups per CU
+  int form;
 };
-// (row pitch, 16-position blocks per wave, load stages, lean form)
-constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3, false}, {16, 7, 2, false}, {16, 4, 3, false}, {8, 2, 3, false},
-                                 {8, 4, 3, false},  {32, 4, 3, false}, {16, 7, 2, true},  {16, 4, 2, true},
-                                 {8, 2, 2, true},   {8, 4, 2, true},   {32, 4, 2, true},  {16, 7, 3, true}};
+// (row pitch, 16-position blocks per wave, load stages, form)
+constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3, kFull}, {16, 7, 2, kFull}, {16, 4, 3, kFull}, {8, 2, 3, kFull},
+                                 {8, 4, 3, kFull},  {32, 4, 3, kFull}, {16, 7, 2, kLean}, {16, 4, 2, kLean},
+                                 {8, 2, 2, kLean},  {8, 4, 2, kLean},  {32, 4, 2, kLean}, {16, 7, 3, kLean}};
 constexpr int kSlabN = int(sizeof(kSlabCfgs) / sizeof(kSlabCfgs[0]));
 
 template <int I>
 struct CfgT {
   static constexpr int P = kSlabCfgs[I].P, NBW = kSlabCfgs[I].NBW, NST = kSlabCfgs[I].NST;
-  static constexpr bool LEAN = kSlabCfgs[I].lean;
+  static constexpr int FORM = kSlabCfgs[I].form;
   using Sh = SlabShape<P, NBW, NST>;
+  static constexpr int LDS = Sh::LDS;
 };
 
 typedef void (*SlabFn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, SlabGeom);
@@ -862,7 +866,7 @@ typedef void (*SlabFn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16
 template <int I>
 SlabFn pick_fn(bool bf, int mode) {
   using C = CfgT<I>;
-  if constexpr (C::LEAN) {
+  if constexpr (C::FORM == kLean) {
     if (mode == kDma4)
       return bf ? &slab_lean_kernel<Bf16, C::P, C::NBW, C::NST> : &slab_lean_kernel<Fp16, C::P, C::NBW, C::NST>;
     return nullptr;
@@ -884,7 +888,7 @@ struct SlabShapeInfo {
 template <int I>
 SlabShapeInfo shape_of() {
   using Sh = typename CfgT<I>::Sh;
-  return SlabShapeInfo{CfgT<I>::P, Sh::RB, Sh::CS, Sh::NT, Sh::LDS};
+  return SlabShapeInfo{CfgT<I>::P, Sh::RB, Sh::CS, Sh::NT, CfgT<I>::LDS};
 }
 
 template <int... Is>
@@ -1062,8 +1066,8 @@ extern "C" int gie_hip_slab_config_get(int index, gie_slab_config* out) {
   out->pitch = c.P;
   out->tile_k = 32;
   out->stages = c.NST;
-  out->workgroups_per_cu = c.lean && sp.lds <= 80 * 1024 ? 2 : 1;
-  out->lean = c.lean ? 1 : 0;
+  out->workgroups_per_cu = c.form == kLean && sp.lds <= 80 * 1024 ? 2 : 1;
+  out->form = c.form;
   out->threads = sp.nt;
   out->lds_bytes = sp.lds;
   out->version = 4;

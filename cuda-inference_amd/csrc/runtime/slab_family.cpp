@@ -194,14 +194,15 @@ void register_slab_family(std::vector<KernelDesc>& out) {
     KernelDesc k;
     k.name = std::string("slab_") + to_string(en.precision) + "_3x3_" + std::to_string(en.info.tile_m) + "x" +
              std::to_string(en.info.rows) + "r" + std::to_string(en.info.pitch) + "_k" +
-             std::to_string(en.info.tile_k) + "_s" + std::to_string(en.info.stages) + (en.info.lean ? "_l" : "") +
+             std::to_string(en.info.tile_k) + "_s" + std::to_string(en.info.stages) +
+             (en.info.form == 1 ? "_l" : "") +
              (en.info.workgroups_per_cu > 1 ? "_o" + std::to_string(en.info.workgroups_per_cu) : std::string()) + "_sk" +
              std::to_string(en.split);
     k.backend = Backend::kTensorCore;
     k.version = en.info.version;
     k.params = {{"block_m", en.info.tile_m}, {"rows", en.info.rows}, {"pitch", en.info.pitch},
                 {"block_k", en.info.tile_k}, {"kernel_h", 3}, {"kernel_w", 3}, {"stages", en.info.stages},
-                {"workgroups_per_cu", en.info.workgroups_per_cu}, {"lean", en.info.lean},
+                {"workgroups_per_cu", en.info.workgroups_per_cu}, {"form", en.info.form},
                 {"split_k", en.split}};
     k.threads_per_block = en.info.threads;
     k.tile_m = en.info.tile_m;

@@ -75,7 +75,7 @@ class GieBandConfig(ctypes.Structure):
 
 class GieSlabConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "rows", "pitch", "tile_k", "stages", "workgroups_per_cu",
-                                            "lean", "threads", "lds_bytes", "version")]
+                                            "form", "threads", "lds_bytes", "version")]
 
 
 class GieDeviceModel(ctypes.Structure):

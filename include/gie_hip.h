@@ -223,7 +223,7 @@ typedef struct gie_slab_config {
   int tile_m, rows, pitch, tile_k;
   int stages;
   int workgroups_per_cu; /* resident workgroups per CU: 2 for the lean form with at most 80 KiB LDS */
-  int lean;              /* 1: the lean form (at most 256 VGPR+AGPR per lane, single-buffered fragments) */
+  int form;              /* 0: double-buffered fragments; 1: lean (single fragment set, at most 256 VGPR+AGPR) */
   int threads;
   int lds_bytes;
   int version;
