@@ -33,9 +33,11 @@
 // tile in LDS, then contiguous NCHW runs per filter (8-byte stores when aligned). split > 1: FP32 partials
 // partial[z][NCHW] over the z-th range of channel slices [floor(S*z/split), floor(S*(z+1)/split)), the partition of
 // src/kernels/tensor_core_mma.cu:112-115, reduced by splitk_reduce.hip.
-// Grid: units (split, image, slab, 32-filter block), filter block fastest; XCD x (slot mod 8) takes a contiguous
-// range of units, so each XCD's L2 holds few images and every filter block.
+// Grid: units (split range, image, slab, 32-filter block); XCD x (slot mod 8) takes a contiguous range of units, with
+// the filter block fastest when that fetches fewer bytes per XCD (config 2: each XCD holds 4 images and every weight)
+// or the image fastest (weight-heavy layers such as config 5: each XCD holds a few filter blocks and every image).
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <mutex>
 
@@ -56,12 +58,31 @@ struct SlabGeom {
   int y_vec;                   // outputs leave as 4-byte pixel pairs
   long long total;             // |Y| elements (partial stride)
   float inv_hw, inv_w;         // 1 / HW, 1 / W for fdiv
-  unsigned mg_ob, mg_band, mg_b;  // n / d = (umulhi(n, mg) + n) >> sh for d = n_ob, n_bands, B (n < 2^30)
-  int sh_ob, sh_band, sh_b;
+  // unit = ((z * rad[2] + d2) * rad[1] + d1) * rad[0] + d0 with d1 = slab; order 0: d0 = filter block, d2 = image
+  // (each XCD's range of units shares images), order 1: d0 = image, d2 = filter block (shares weights)
+  int order;
+  int rad[3];
+  unsigned mg[3];  // n / rad[k] = (umulhi(n, mg[k]) + n) >> sh[k] for n < 2^30
+  int sh[3];
 };
 
 __device__ __forceinline__ int magic_div(int n, unsigned mg, int sh) {
   return int((__umulhi(unsigned(n), mg) + unsigned(n)) >> sh);
+}
+
+struct SlabUnit {
+  int b, z, ob, band;
+};
+__device__ __forceinline__ SlabUnit decode_unit(int unit, const SlabGeom& g) {
+  const int q0 = magic_div(unit, g.mg[0], g.sh[0]), d0 = unit - q0 * g.rad[0];
+  const int q1 = magic_div(q0, g.mg[1], g.sh[1]), d1 = q0 - q1 * g.rad[1];
+  const int z = magic_div(q1, g.mg[2], g.sh[2]), d2 = q1 - z * g.rad[2];
+  SlabUnit u;
+  u.z = z;
+  u.band = d1;
+  u.ob = g.order == 0 ? d0 : d2;
+  u.b = g.order == 0 ? d2 : d0;
+  return u;
 }
 
 template <int P, int NBW, int NST>
@@ -300,13 +321,9 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
   const int slot = int(blockIdx.x);
   const int unit = (slot >> 3) + (slot & 7) * g.per_xcd;
   if (unit >= g.n_units) return;  // workgroup-uniform
-  int rest = unit;
-  const int ob = rest % g.n_ob;
-  rest /= g.n_ob;
-  const int band = rest % g.n_bands;
-  rest /= g.n_bands;
-  const int b = rest % g.B, z = rest / g.B;
-  const int o0 = ob * kSlTO, oh0 = band * RB;
+  const SlabUnit un = decode_unit(unit, g);
+  const int b = un.b, z = un.z;
+  const int o0 = un.ob * kSlTO, oh0 = un.band * RB;
   const int s_beg = (g.S * z) / g.split, ns = (g.S * (z + 1)) / g.split - s_beg;
   const int nrows = min(RB, g.H - oh0);
 
@@ -680,10 +697,9 @@ __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __res
   const int slot = int(blockIdx.x);
   const int unit = (slot >> 3) + (slot & 7) * g.per_xcd;
   if (unit >= g.n_units) return;
-  const int q_ob = magic_div(unit, g.mg_ob, g.sh_ob), ob = unit - q_ob * g.n_ob;
-  const int q_band = magic_div(q_ob, g.mg_band, g.sh_band), band = q_ob - q_band * g.n_bands;
-  const int z = magic_div(q_band, g.mg_b, g.sh_b), b = q_band - z * g.B;
-  const int o0 = ob * kSlTO, oh0 = band * RB;
+  const SlabUnit un = decode_unit(unit, g);
+  const int b = un.b, z = un.z;
+  const int o0 = un.ob * kSlTO, oh0 = un.band * RB;
   int s_beg = 0, ns = g.S;
   if (g.split > 1) {
     s_beg = (g.S * z) / g.split;
@@ -956,9 +972,18 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
     *sh = l;
     *mg = unsigned((((1ULL << l) - unsigned(d)) << 32) / unsigned(d) + 1);
   };
-  magic(g.n_ob, &g.mg_ob, &g.sh_ob);
-  magic(g.n_bands, &g.mg_band, &g.sh_band);
-  magic(g.B, &g.mg_b, &g.sh_b);
+  // unit order: the one whose XCD ranges (per_xcd consecutive units) fetch fewer bytes into their L2 — filter block
+  // fastest shares images (few images x every weight), image fastest shares weights (few filter blocks x every image)
+  const double wz = 32.0 * gg->in_channels * 18.0 / split;           // one filter block's weights per channel range
+  const double xz = 2.0 * gg->in_channels * double(hw) / split / bands;  // one slab's planes per channel range
+  const double per = double(g.per_xcd);
+  const double by_ob = std::min(double(g.n_ob), per) * wz + std::ceil(per / g.n_ob) * xz;
+  const double by_b = std::min(double(g.B) * bands, per) * xz + std::ceil(per / (double(g.B) * bands)) * wz;
+  g.order = by_b < by_ob ? 1 : 0;
+  g.rad[0] = g.order == 0 ? g.n_ob : g.B;
+  g.rad[1] = g.n_bands;
+  g.rad[2] = g.order == 0 ? g.B : g.n_ob;
+  for (int k = 0; k < 3; ++k) magic(g.rad[k], &g.mg[k], &g.sh[k]);
   g.x_bytes = int(xb), g.w_bytes = int(wb);
   g.relu = gg->relu;
   g.split = split;
