@@ -238,6 +238,8 @@ def dominant_kernel(registry_name: str) -> str:
     """The device function that does the multiply-accumulate work for a registry kernel (the rocprof kernel name)."""
     if registry_name.startswith("slab_") and "_l_" in registry_name:
         return "slab_lean_kernel (3x3 MFMA convolution straight from NCHW / OIHW, lean form, conv_slab.hip)"
+    if registry_name.startswith("slab_") and "_p_" in registry_name:
+        return "slab_pipe_kernel (3x3 MFMA convolution straight from NCHW / OIHW, pipelined form, conv_slab.hip)"
     stems = [("slab_", "slab_kernel (3x3 MFMA convolution straight from NCHW / OIHW, conv_slab.hip)"),
              ("band_", "band_kernel (band MFMA convolution straight from NCHW, conv_band.hip)"),
              ("halo_", "halo_kernel (halo-tiled MFMA implicit GEMM, conv_halo.hip)"),

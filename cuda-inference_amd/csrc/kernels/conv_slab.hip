@@ -854,9 +854,226 @@ __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __res
   slab_store<E, P, NBW>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
 }
 
+// ---- pipelined form: one workgroup per CU, every slot of the MFMA stream carrying the side work ----
+// With one wave per SIMD a wave issues one instruction per 4-cycle slot, and a 16 x 16 x 32 MFMA occupies the
+// matrix core for 4 slots: the 3 slots behind each MFMA are the only room for everything else. Left to itself the
+// compiler emits each tap's MFMAs back to back and the side work (fragment transposes, the next slice's loads) as one
+// clump after them, during which the matrix core idles. This form fixes the order: step j multiplies slice j from
+// registers while slice j + 1 is read from LDS and transposed into the other fragment set and slice j + NST loads
+// into the stage slice j occupied, one MFMA per slot followed by at most a few of those instructions. The step's
+// only wait is at its start (slice j + 1 landed for this wave, then the barrier for all waves), so each slice's loads
+// have NST - 1 steps to land. Loads for slices past the last one go through zero-length buffer resources: they
+// write zeros into a stage no later step multiplies, and every step counts the same number of loads.
+// Whole 32-channel slices only (C % 32 == 0), even rows (4-byte direct loads).
+template <int P, int NBW>
+struct PipeSched {
+  static constexpr int G = P >= 16 ? 16 : P;
+  static constexpr int NBR = (16 * (NBW - 1) + 2 * P) / G + 1;
+  static constexpr int NM = 9 * NBW;                         // MFMAs per slice: tap-major, NBW blocks per tap
+  static constexpr int NRD = 9 + 2 * NBR;                    // LDS reads per slice: 9 weight runs, then pixel halves
+  static constexpr int NRS = NRD < NM ? NRD : NM;            // slots carrying reads
+  static constexpr int PB = NRD < NM - 1 ? NRD : NM - 1;     // first slot carrying a transpose (after every read)
+  static constexpr int rd_slot(int q) { return q * NRS / NRD; }
+  static constexpr int perm_slot(int p) { return PB + p * (NM - PB) / 36; }
+  static constexpr int load_slot(int q, int ni) { return q * NM / ni; }
+};
+
+template <typename F, int... K>
+__device__ __forceinline__ void for_seq(F&& f, std::integer_sequence<int, K...>) {
+  (f(std::integral_constant<int, K>{}), ...);
+}
+
+template <typename E, int P, int NBW, int NST>
+__global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                          float* __restrict__ partial, SlabGeom g) {
+  using Sh = SlabShape<P, NBW, NST>;
+  using Sc = PipeSched<P, NBW>;
+  constexpr int CS = Sh::CS, NW = Sh::NW, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G, NBR = Sh::NBR;
+  constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
+  constexpr int ACT = Sh::ACT, KA = Sh::KA, R = Sh::R;
+  constexpr int WOFF = NST * ACT;  // LDS: [NST activation stages][NST weight stages]
+  constexpr int NI = KBW + KA;     // loads per wave per slice
+  constexpr int NM = Sc::NM, NRD = Sc::NRD;
+  constexpr int U = NST % 2 == 0 ? NST : 2 * NST;  // steps per loop turn: fragment set and stages are constants
+  static_assert(NST >= 3, "a slice loads NST - 1 steps ahead of its use");
+  static_assert((NST - 1) * NI + 4 < 64, "loads in flight (and the bias loads) fit the vmcnt counter");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fh = wave & 1, wr = wave >> 1;
+
+  const int slot = int(blockIdx.x);
+  const int unit = (slot >> 3) + (slot & 7) * g.per_xcd;
+  if (unit >= g.n_units) return;
+  const SlabUnit un = decode_unit(unit, g);
+  const int b = un.b, z = un.z;
+  const int o0 = un.ob * kSlTO, oh0 = un.band * RB;
+  int s_beg = 0, ns = g.S;
+  if (g.split > 1) {
+    s_beg = (g.S * z) / g.split;
+    ns = (g.S * (z + 1)) / g.split - s_beg;
+  }
+  const int nrows = min(RB, g.H - oh0);
+
+  const v4i xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
+  const v4i x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: loads give zeros
+  const unsigned lds0 = lds_addr(lds);
+
+  const int f0 = o0 + fh * 16 + 4 * (lane >> 4);
+  uint32_t bbits[4];
+  {
+    const v4i br = make_vsharp(bias, g.split == 1 && bias != nullptr ? 2 * g.O : 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bbits[i] = load2s(br, 2 * min(f0 + i, g.O - 1), 0);
+  }
+
+  int w_voff[KBW];
+#pragma unroll
+  for (int kb = 0; kb < KBW; ++kb) {
+    const int u = (wave + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
+    w_voff[kb] = (f < kSlTO && k < WCH && o0 + f < g.O) ? (o0 + f) * g.C * 18 + 16 * k : kOut;
+  }
+  constexpr int NV = 4 * R;
+  int a_voff[NV];
+  {
+    const int swz_hi = (wave & 1) << 2;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int seg = (v % R) * 8 + (lane >> 3);
+      const int pos = ((seg ^ ((v / R) | swz_hi)) << 4) + 2 * (lane & 7);
+      const int row = pos / P, col = pos % P, ih = oh0 - 1 + row;
+      a_voff[v] = (row < NR && ih >= 0 && ih < g.H && col < g.W) ? (ih * g.W + col) * 2 : kOut;
+    }
+  }
+  const int hw2 = g.HW * 2;
+  const int a_soff0 = (b * g.C + s_beg * CS + 8 * wave) * hw2;  // + slice * CS * hw2 + (q / R) * hw2
+  const int w_soff0 = s_beg * CS * 18;                           // + slice * CS * 18
+
+  // load q of slice s (relative to s_beg) into stage ST: q < KA this wave's activation rows, then its weight blocks
+  struct SliceArgs {
+    v4i xs, ws;
+    int a_soff, w_soff;
+  };
+  auto slice_args = [&](int s) __attribute__((always_inline)) {
+    const bool real = s < ns;
+    return SliceArgs{real ? xr : x0, real ? wrs : w0, real ? a_soff0 + s * CS * hw2 : 0, real ? w_soff0 + s * CS * 18 : 0};
+  };
+  auto load_one = [&](auto qc, auto st_c, const SliceArgs& sa) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value, ST = decltype(st_c)::value;
+    if constexpr (q < KA) {
+      dma4s(sa.xs, lds0 + unsigned(ST * ACT + (wave * KA + q) * 256), a_voff[(q % R) + R * ((q / R) & 3)],
+            sa.a_soff + (q / R) * hw2);
+    } else {
+      constexpr int kb = q - KA;
+      dma16s(sa.ws, lds0 + unsigned(WOFF + ST * WST + (wave + NW * kb) * 1024), w_voff[kb], sa.w_soff);
+    }
+  };
+  auto load_slice = [&](int s, auto st_c) __attribute__((always_inline)) {
+    const SliceArgs sa = slice_args(s);
+    for_seq([&](auto qc) __attribute__((always_inline)) { load_one(qc, st_c, sa); },
+            std::make_integer_sequence<int, NI>{});
+  };
+
+  const unsigned a_rd = lds0 + unsigned(WOFF + (fh * 16 + (lane & 15)) * WPITCH + 8 * (lane >> 4) * 18);
+  unsigned b_rd[NBR][2];
+#pragma unroll
+  for (int u = 0; u < NBR; ++u) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ch = 8 * (lane >> 4) + 4 * h + ((lane & 15) >> 2);
+      const int pos = wr * RW * P + u * G + 4 * (lane & 3);
+      b_rd[u][h] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
+    }
+  }
+
+  f32x4 acc[3][NBW];
+#pragma unroll
+  for (int s2 = 0; s2 < 3; ++s2) {
+#pragma unroll
+    for (int j2 = 0; j2 < NBW; ++j2) acc[s2][j2] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  u32x4 fw[2][9], fb[2][NBR];
+  uint32_t d[36];
+  // read q of the slice in stage ST into fragment set S: q < 9 the lane's 16-byte piece t = q of its weight run,
+  // then pixel block (q - 9) / 2, channel quad (q - 9) % 2
+  auto read_one = [&](auto qc, auto st_c, auto set_c) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value, ST = decltype(st_c)::value, S = decltype(set_c)::value;
+    if constexpr (q < 9) {
+      const u32x4 v = rd16(a_rd + unsigned(ST * WST + 16 * q));
+      d[4 * q] = v.x, d[4 * q + 1] = v.y, d[4 * q + 2] = v.z, d[4 * q + 3] = v.w;
+    } else {
+      constexpr int u = (q - 9) / 2, h = (q - 9) % 2;
+      const u32x2 v = rd_tr(b_rd[u][h] + unsigned(ST * ACT));
+      fb[S][u][2 * h] = v.x;
+      fb[S][u][2 * h + 1] = v.y;
+    }
+  };
+  // transpose p: dword p % 4 of tap p / 4's weight fragment (8 channels of one tap per lane)
+  auto perm_one = [&](auto pc, auto set_c) __attribute__((always_inline)) {
+    constexpr int p = decltype(pc)::value, S = decltype(set_c)::value, t = p / 4, c = p % 4;
+    fw[S][t][c] = pick2(d, 18 * c + t, 18 * c + 9 + t);
+  };
+  auto mfma_one = [&](auto kc, auto set_c) __attribute__((always_inline)) {
+    constexpr int k = decltype(kc)::value, S = decltype(set_c)::value;
+    constexpr int t = k / NBW, j = k % NBW, r = t / 3, sc = t % 3;
+    acc[sc][j] = E::mfma(fw[S][t], fb[S][(16 * j + r * P) / G], acc[sc][j]);
+  };
+
+  // ---- prologue: slices 0 .. NST-1 loading, slice 0 read into set 0 ----
+  for_seq([&](auto sc) __attribute__((always_inline)) {
+    constexpr int s = decltype(sc)::value;
+    if constexpr (s == NST - 1) wait_vmcnt<(NST - 2) * NI>();  // bias and slice 0 landed: room for the last stage
+    load_slice(s, std::integral_constant<int, s>{});
+  }, std::make_integer_sequence<int, NST>{});
+  stage_barrier();  // slice 0 has landed for every wave
+  for_seq([&](auto qc) __attribute__((always_inline)) {
+    read_one(qc, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+  }, std::make_integer_sequence<int, NRD>{});
+  for_seq([&](auto pc) __attribute__((always_inline)) { perm_one(pc, std::integral_constant<int, 0>{}); },
+          std::make_integer_sequence<int, 36>{});
+
+  // ---- step j (u = j mod U): slice j multiplies from set u % 2 ----
+  auto step = [&](int j, auto u_c) __attribute__((always_inline)) {
+    constexpr int uu = decltype(u_c)::value;
+    constexpr int cur = uu & 1, nxt = cur ^ 1, st_rd = (uu + 1) % NST, st_ld = uu % NST;
+    wait_vmcnt<(NST - 2) * NI>();  // this wave's loads of slice j + 1 have landed (slices j+2 .. j+NST-1 in flight)
+    stage_barrier();               // ... every wave's, and every wave has read slice j out of stage st_ld
+    const SliceArgs sa = slice_args(j + NST);
+    __builtin_amdgcn_sched_barrier(0);
+    for_seq([&](auto kc) __attribute__((always_inline)) {
+      constexpr int k = decltype(kc)::value;
+      mfma_one(kc, std::integral_constant<int, cur>{});
+      for_seq([&](auto qc) __attribute__((always_inline)) {
+        if constexpr (Sc::rd_slot(decltype(qc)::value) == k)
+          read_one(qc, std::integral_constant<int, st_rd>{}, std::integral_constant<int, nxt>{});
+      }, std::make_integer_sequence<int, NRD>{});
+      for_seq([&](auto qc) __attribute__((always_inline)) {
+        if constexpr (Sc::load_slot(decltype(qc)::value, NI) == k)
+          load_one(qc, std::integral_constant<int, st_ld>{}, sa);
+      }, std::make_integer_sequence<int, NI>{});
+      for_seq([&](auto pc) __attribute__((always_inline)) {
+        if constexpr (Sc::perm_slot(decltype(pc)::value) == k) perm_one(pc, std::integral_constant<int, nxt>{});
+      }, std::make_integer_sequence<int, 36>{});
+      __builtin_amdgcn_sched_barrier(0);
+    }, std::make_integer_sequence<int, NM>{});
+  };
+  for (int j = 0; j < ns; j += U) {
+    for_seq([&](auto uc) __attribute__((always_inline)) {
+      if (j + decltype(uc)::value < ns) step(j + decltype(uc)::value, uc);
+    }, std::make_integer_sequence<int, U>{});
+  }
+  wait_vmcnt<0>();  // the zero loads past the last slice (and the bias loads, long landed)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) touch_v(bbits[i]);
+  slab_store<E, P, NBW>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
+}
+
 // kernel forms: slab_kernel (double-buffered fragments), slab_lean_kernel (single fragment set, at most 256
-// VGPR+AGPR)
-constexpr int kFull = 0, kLean = 1;
+// VGPR+AGPR), slab_pipe_kernel (double-buffered fragments, fixed slot schedule, whole slices)
+constexpr int kFull = 0, kLean = 1, kPipe = 2;
 struct SlabCfg {
   int P, NBW, NST;
   int form;
@@ -864,7 +1081,8 @@ struct SlabCfg {
 // (row pitch, 16-position blocks per wave, load stages, form)
 constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3, kFull}, {16, 7, 2, kFull}, {16, 4, 3, kFull}, {8, 2, 3, kFull},
                                  {8, 4, 3, kFull},  {32, 4, 3, kFull}, {16, 7, 2, kLean}, {16, 4, 2, kLean},
-                                 {8, 2, 2, kLean},  {8, 4, 2, kLean},  {32, 4, 2, kLean}, {16, 7, 3, kLean}};
+                                 {8, 2, 2, kLean},  {8, 4, 2, kLean},  {32, 4, 2, kLean}, {16, 7, 3, kLean},
+                                 {16, 7, 3, kPipe}, {16, 4, 3, kPipe}};
 constexpr int kSlabN = int(sizeof(kSlabCfgs) / sizeof(kSlabCfgs[0]));
 
 template <int I>
@@ -885,6 +1103,10 @@ SlabFn pick_fn(bool bf, int mode) {
   if constexpr (C::FORM == kLean) {
     if (mode == kDma4)
       return bf ? &slab_lean_kernel<Bf16, C::P, C::NBW, C::NST> : &slab_lean_kernel<Fp16, C::P, C::NBW, C::NST>;
+    return nullptr;
+  } else if constexpr (C::FORM == kPipe) {
+    if (mode == kDma4)
+      return bf ? &slab_pipe_kernel<Bf16, C::P, C::NBW, C::NST> : &slab_pipe_kernel<Fp16, C::P, C::NBW, C::NST>;
     return nullptr;
   } else {
     if (mode == kDma4)
@@ -931,6 +1153,7 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   if (gg->batch <= 0 || gg->in_channels <= 0 || gg->out_channels <= 0 || gg->in_h <= 0 || gg->in_w <= 0)
     return GIE_HIP_EINVAL;
   if (gg->in_channels % 8 != 0) return GIE_HIP_EUNSUPPORTED;  // 16-byte chunks of the weight runs
+  if (kSlabCfgs[cfg].form == kPipe && gg->in_channels % 32 != 0) return GIE_HIP_EUNSUPPORTED;  // whole slices
   const long long hw = 1LL * gg->in_h * gg->in_w;
   const bool bf = dtype == GIE_HIP_BF16;
   SlabShapeInfo si{};
@@ -1095,7 +1318,7 @@ extern "C" int gie_hip_slab_config_get(int index, gie_slab_config* out) {
   out->form = c.form;
   out->threads = sp.nt;
   out->lds_bytes = sp.lds;
-  out->version = 4;
+  out->version = 5;
   return GIE_HIP_OK;
 }
 

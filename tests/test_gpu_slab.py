@@ -90,6 +90,9 @@ CASES = [
     (2, 64, 28, 28, 48, "fp16", True, True, 1, 0, 0),     # 28-wide rows, several slabs
     (1, 32, 5, 3, 8, "bf16", False, False, 1, 0, 0),      # tiny: one slice of 32 real channels
     (2, 8, 6, 6, 5, "fp16", True, True, 1, 0, 0),         # C = 8
+    (1, 32, 10, 10, 32, "fp16", True, True, 1, 0, 0),     # one slice: fewer slices than load stages
+    (2, 96, 12, 14, 64, "bf16", True, True, 2, 0, 0),     # split-K 2 over 3 slices (ranges of 1 and 2)
+    (3, 320, 14, 8, 72, "fp16", True, False, 1, 0, 0),    # 10 slices: a partial loop turn, O past two blocks
 ]
 
 
