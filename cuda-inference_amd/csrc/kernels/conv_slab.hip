@@ -73,6 +73,18 @@ __device__ __forceinline__ int magic_div(int n, unsigned mg, int sh) {
 struct SlabUnit {
   int b, z, ob, band;
 };
+
+// Every kernel argument the set-up and the epilogue read, requested before the first branch: the compiler otherwise
+// issues the argument loads per basic block (the unit count for the early exit, then the geometry, then the
+// pointers), three round trips to the argument segment of several hundred cycles each instead of one.
+__device__ __forceinline__ void args_in_sgprs(const void* x, const void* w, const void* bias, const void* y,
+                                              const void* partial, const SlabGeom& g) {
+  asm volatile("" ::"s"(x), "s"(w), "s"(bias), "s"(y), "s"(partial));
+  asm volatile("" ::"s"(g.n_units), "s"(g.per_xcd), "s"(g.order), "s"(g.rad[0]), "s"(g.rad[1]), "s"(g.rad[2]),
+               "s"(g.mg[0]), "s"(g.mg[1]), "s"(g.mg[2]), "s"(g.sh[0]), "s"(g.sh[1]), "s"(g.sh[2]));
+  asm volatile("" ::"s"(g.S), "s"(g.split), "s"(g.C), "s"(g.H), "s"(g.W), "s"(g.HW), "s"(g.O), "s"(g.x_bytes),
+               "s"(g.w_bytes), "s"(g.relu), "s"(g.y_vec), "s"(g.total));
+}
 __device__ __forceinline__ SlabUnit decode_unit(int unit, const SlabGeom& g) {
   const int q0 = magic_div(unit, g.mg[0], g.sh[0]), d0 = unit - q0 * g.rad[0];
   const int q1 = magic_div(q0, g.mg[1], g.sh[1]), d1 = q0 - q1 * g.rad[1];
@@ -221,17 +233,29 @@ __device__ __forceinline__ void store2(v4i rsrc, int voff, uint32_t v) {
 // Epilogue of one unit, shared by the slab kernels: tap-column shifts (DPP), then split 1: bias + ReLU + one rounding
 // and pixel-pair (or 2-byte) stores straight from the accumulators; split > 1: FP32 partials. One loop per store
 // form; positions outside the image and filters past O store to kOut (dropped), so no lane is masked by branches.
-template <typename E, int P, int NBW>
+// PADS_LOADED: the padding columns of the LDS rows hold whatever the row loads brought in (16-byte loads run past
+// the row end into them); the left neighbour of column 0 and the right neighbour of column W - 1 are padding, so those
+// two shifted terms are selected out instead of read as zeros.
+template <typename E, int P, int NBW, bool PADS_LOADED = false>
 __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uint32_t (&bbits)[4], int lane, int wr,
                                            int oh0, int nrows, int b, int z, int o0, int f0,
                                            uint16_t* __restrict__ y, float* __restrict__ partial, const SlabGeom& g) {
   constexpr int RW = 16 * NBW / P;
   (void)o0;
   auto column = [&](int j) __attribute__((always_inline)) {
-    f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
-    if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
-    if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
-    return out;
+    if constexpr (PADS_LOADED) {
+      f32x4 t0 = dpp4<kShr1>(acc[0][j]), t2 = dpp4<kShl1>(acc[2][j]);
+      if (j > 0) t0 += dpp4<kShl15>(acc[0][j - 1]);
+      if (j + 1 < NBW) t2 += dpp4<kShr15>(acc[2][j + 1]);
+      const int c = (wr * RW * P + 16 * j + (lane & 15)) % P;
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      return acc[1][j] + (c != 0 ? t0 : zero) + (c != g.W - 1 ? t2 : zero);
+    } else {
+      f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
+      if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
+      if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
+      return out;
+    }
   };
   const int nf = g.O - f0;                         // filters of the lane's four that exist (>= 4: all)
   const int fbase = (b * g.O + f0) * g.HW;         // element index of (b, f0, 0)
@@ -864,7 +888,10 @@ __global__ __launch_bounds__(256, 2) void slab_lean_kernel(const uint16_t* __res
 // only wait is at its start (slice j + 1 landed for this wave, then the barrier for all waves), so each slice's loads
 // have NST - 1 steps to land. Loads for slices past the last one go through zero-length buffer resources: they
 // write zeros into a stage no later step multiplies, and every step counts the same number of loads.
-// Whole 32-channel slices only (C % 32 == 0), even rows (4-byte direct loads).
+// Activations load 16 bytes (8 positions) per lane, a quarter of the load instructions of 4-byte loads: the address
+// work per load instruction, not the bytes, bounds how fast a CU issues them. A chunk may run past its row's end into
+// the padding positions, so the epilogue selects out the two shifted terms that would read them.
+// Whole 32-channel slices only (C % 32 == 0), even rows and a 4-byte aligned x (4-byte aligned 16-byte chunks).
 template <int P, int NBW>
 struct PipeSched {
   static constexpr int G = P >= 16 ? 16 : P;
@@ -892,14 +919,17 @@ __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __res
   using Sc = PipeSched<P, NBW>;
   constexpr int CS = Sh::CS, NW = Sh::NW, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G, NBR = Sh::NBR;
   constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
-  constexpr int ACT = Sh::ACT, KA = Sh::KA, R = Sh::R;
-  constexpr int WOFF = NST * ACT;  // LDS: [NST activation stages][NST weight stages]
-  constexpr int NI = KBW + KA;     // loads per wave per slice
+  constexpr int ACT = Sh::ACT;
+  constexpr int WOFF = NST * ACT;      // LDS: [NST activation stages][NST weight stages]
+  constexpr int KA = ACT / 1024 / NW;  // 16-byte activation loads per wave per slice, two channel regions each
+  static_assert(CHP == 512 && KA * 2 == 8, "a wave's 8 channels take KA loads of two 512-byte channel regions");
+  constexpr int NI = KBW + KA;         // loads per wave per slice
   constexpr int NM = Sc::NM, NRD = Sc::NRD;
   constexpr int U = NST % 2 == 0 ? NST : 2 * NST;  // steps per loop turn: fragment set and stages are constants
   static_assert(NST >= 3, "a slice loads NST - 1 steps ahead of its use");
   static_assert((NST - 1) * NI + 4 < 64, "loads in flight (and the bias loads) fit the vmcnt counter");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+  args_in_sgprs(x, w, bias, y, partial, g);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -930,22 +960,29 @@ __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __res
     for (int i = 0; i < 4; ++i) bbits[i] = load2s(br, 2 * min(f0 + i, g.O - 1), 0);
   }
 
+  // per-lane load offsets, worked out branch-free (value, then a select) so the first loads go out early
   int w_voff[KBW];
+  const int wrow = g.C * 18;  // bytes of one filter's OIHW weights
 #pragma unroll
   for (int kb = 0; kb < KBW; ++kb) {
     const int u = (wave + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
-    w_voff[kb] = (f < kSlTO && k < WCH && o0 + f < g.O) ? (o0 + f) * g.C * 18 + 16 * k : kOut;
+    const int val = (o0 + f) * wrow + 16 * k;
+    const bool ok = (f < kSlTO) & (k < WCH) & (o0 + f < g.O);
+    w_voff[kb] = ok ? val : kOut;
   }
-  constexpr int NV = 4 * R;
-  int a_voff[NV];
+  // activations: 16 bytes (8 positions) per lane; lane = (channel cl of the load's pair, segment slot, half). A chunk
+  // that starts inside a row may run past its end into the padding positions (the epilogue never reads them there);
+  // rows outside the image load zeros. Load q covers channels 8 * wave + 2q + cl, whose swizzle depends on q % 2 only.
+  int a_voff[2];
   {
-    const int swz_hi = (wave & 1) << 2;
+    const int cl = lane >> 5, sslot = (lane >> 1) & 15, half = lane & 1;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int seg = (v % R) * 8 + (lane >> 3);
-      const int pos = ((seg ^ ((v / R) | swz_hi)) << 4) + 2 * (lane & 7);
+    for (int e = 0; e < 2; ++e) {
+      const int pos = ((sslot ^ seg_swz(8 * wave + 2 * e + cl)) << 4) + 8 * half;
       const int row = pos / P, col = pos % P, ih = oh0 - 1 + row;
-      a_voff[v] = (row < NR && ih >= 0 && ih < g.H && col < g.W) ? (ih * g.W + col) * 2 : kOut;
+      const int val = (cl * g.HW + ih * g.W + col) * 2;
+      const bool ok = (row < NR) & (unsigned(ih) < unsigned(g.H)) & (col < g.W);
+      a_voff[e] = ok ? val : kOut;
     }
   }
   const int hw2 = g.HW * 2;
@@ -964,8 +1001,7 @@ __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __res
   auto load_one = [&](auto qc, auto st_c, const SliceArgs& sa) __attribute__((always_inline)) {
     constexpr int q = decltype(qc)::value, ST = decltype(st_c)::value;
     if constexpr (q < KA) {
-      dma4s(sa.xs, lds0 + unsigned(ST * ACT + (wave * KA + q) * 256), a_voff[(q % R) + R * ((q / R) & 3)],
-            sa.a_soff + (q / R) * hw2);
+      dma16s(sa.xs, lds0 + unsigned(ST * ACT + (wave * KA + q) * 1024), a_voff[q & 1], sa.a_soff + 2 * q * hw2);
     } else {
       constexpr int kb = q - KA;
       dma16s(sa.ws, lds0 + unsigned(WOFF + ST * WST + (wave + NW * kb) * 1024), w_voff[kb], sa.w_soff);
@@ -976,6 +1012,11 @@ __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __res
     for_seq([&](auto qc) __attribute__((always_inline)) { load_one(qc, st_c, sa); },
             std::make_integer_sequence<int, NI>{});
   };
+
+  // ---- prologue: slices 0 .. NST-2 start loading before any fragment address is worked out ----
+  for_seq([&](auto sc) __attribute__((always_inline)) { load_slice(decltype(sc)::value, sc); },
+          std::make_integer_sequence<int, NST - 1>{});
+  __builtin_amdgcn_sched_barrier(0);
 
   const unsigned a_rd = lds0 + unsigned(WOFF + (fh * 16 + (lane & 15)) * WPITCH + 8 * (lane >> 4) * 18);
   unsigned b_rd[NBR][2];
@@ -1022,12 +1063,10 @@ __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __res
     acc[sc][j] = E::mfma(fw[S][t], fb[S][(16 * j + r * P) / G], acc[sc][j]);
   };
 
-  // ---- prologue: slices 0 .. NST-1 loading, slice 0 read into set 0 ----
-  for_seq([&](auto sc) __attribute__((always_inline)) {
-    constexpr int s = decltype(sc)::value;
-    if constexpr (s == NST - 1) wait_vmcnt<(NST - 2) * NI>();  // bias and slice 0 landed: room for the last stage
-    load_slice(s, std::integral_constant<int, s>{});
-  }, std::make_integer_sequence<int, NST>{});
+  // ---- the last stage loads once the bias and slice 0 have landed (loads in flight stay within the counter); slice 0
+  // is read into set 0 ----
+  wait_vmcnt<(NST - 2) * NI>();
+  load_slice(NST - 1, std::integral_constant<int, NST - 1>{});
   stage_barrier();  // slice 0 has landed for every wave
   for_seq([&](auto qc) __attribute__((always_inline)) {
     read_one(qc, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
@@ -1068,7 +1107,7 @@ __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __res
   wait_vmcnt<0>();  // the zero loads past the last slice (and the bias loads, long landed)
 #pragma unroll
   for (int i = 0; i < 4; ++i) touch_v(bbits[i]);
-  slab_store<E, P, NBW>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
+  slab_store<E, P, NBW, true>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
 }
 
 // kernel forms: slab_kernel (double-buffered fragments), slab_lean_kernel (single fragment set, at most 256
