@@ -3,34 +3,32 @@
 //
 // A workgroup owns 32 output channels x one slab of RB output rows of one image. In LDS the slab's input rows
 // (one halo row above and below) form a flat array of positions, P per row (P >= in_w + 1): input (ih, iw) sits at
-// position q = (ih - oh0 + 1) * P + iw, and positions in_w .. P-1 of every row are zero (they are both the right
-// padding of the row and, seen from the next row, its left padding). Output pixel (oh, ow) has the flat index
-// o = (oh - oh0) * P + ow, and tap (r, s) of it reads position o + r * P + s - 1. A 16 x 16 MFMA block is 16
-// consecutive flat outputs, so the pixel operand of tap row r is one 16-position read at o + r * P for all three
-// tap columns, and the tap column enters through three accumulator sets:
+// position q = (ih - oh0 + 1) * P + iw; positions in_w .. P-1 of every row are padding (the right padding of the row
+// and, seen from the next row, its left padding). Output pixel (oh, ow) has the flat index o = (oh - oh0) * P + ow,
+// and tap (r, s) of it reads position o + r * P + s - 1. A 16 x 16 MFMA block is 16 consecutive flat outputs, so
+// the pixel operand of tap row r is one 16-position read at o + r * P for all three tap columns, and the tap column
+// enters through three accumulator sets:
 //     acc_s[o] = sum_r W[r][s] . X[o + r*P],     y[o] = acc_0[o - 1] + acc_1[o] + acc_2[o + 1],
-// the shifts being DPP lane moves applied once in the epilogue (flat outputs at columns >= in_w are dropped; an
-// accumulator just outside a wave's rows only ever reads padding columns and counts as zero). The inner loop is
-// LDS reads, 36 v_perm per slice and MFMAs.
+// the shifts being DPP lane moves applied once in the epilogue (flat outputs at columns >= in_w are dropped). The
+// inner loop is LDS reads, 36 v_perm per slice and MFMAs.
 //
-// Waves: (filter half fh: 16 filters) x (row half wr: RW = 16 * NBW / P rows = NBW blocks) x (channel half kh,
-// NWK = 2 only: the two 32-channel halves of a 64-channel slice, waves w and w + 4, which share a SIMD and whose
-// sums meet in LDS at the end).
+// Waves: 4 = (filter half fh: 16 filters) x (row half wr: RW = 16 * NBW / P rows = NBW blocks), one per SIMD.
 //
-// Both operands travel by direct-to-LDS loads (no registers), NST stages, one slice in flight per stage:
+// Both operands travel by direct-to-LDS loads, NST stages, one 32-channel slice per stage:
 //   * weights: each filter's OIHW run of the slice (CS x 9 contiguous halves) by 16-byte loads into a staging row
 //     of CS*18 + 16 bytes (the extra 16 bytes spread the rows over the banks). A wave reads its lanes' 144-byte runs
 //     (8 channels x 9 taps of one filter) with 9 ds_read_b128 and transposes them in registers (v_perm) into the 9
 //     tap fragments (8 channels of one tap per lane) — there is no weight repack anywhere;
-//   * activations: 4-byte loads place every channel's input rows at their padded positions directly ([channel][32-
-//     byte segments of 16 positions], segment slot = segment ^ swizzle(channel) so the transposing fragment reads
-//     of 8 channels hit 8 distinct bank groups); out-of-image rows and padding columns load as zeros, so nothing is
-//     ever cleared. The pixel fragments come out with ds_read_b64_tr_b16 (4 channels of 16 positions per 16-lane
-//     group, each lane receiving the 4 channels of its position). Rows of odd width (or x not 4-byte aligned) take
-//     2-byte register loads and 2-byte LDS writes instead, into the same layout (padding cleared once).
-// Epilogue: DPP shift-add of the three accumulator sets, the K halves summed through LDS, bias + ReLU + one RNE
-// rounding (the reference's apply_epilogue order, src/kernels/fused_epilogue.cuh:11-16) into a [filter][pixel]
-// tile in LDS, then contiguous NCHW runs per filter (8-byte stores when aligned). split > 1: FP32 partials
+//   * activations: [channel][32-byte segments of 16 positions], segment slot = segment ^ swizzle(channel) so the
+//     transposing fragment reads of 8 channels hit 8 distinct bank groups; out-of-image rows load as zeros. The
+//     full and lean forms load 4-byte position pairs, padding columns included (as zeros); the pipelined form loads
+//     16-byte chunks of 8 positions, whose tails run into the padding positions, and its epilogue never reads
+//     those. The pixel fragments come out with ds_read_b64_tr_b16 (4 channels of 16 positions per 16-lane group,
+//     each lane receiving the 4 channels of its position). Rows of odd width (or x not 4-byte aligned) take 2-byte
+//     register loads and 2-byte LDS writes instead (full form; padding cleared once).
+// Epilogue (slab_store): the DPP shift-add of the three accumulator sets, then bias + ReLU + one RNE rounding (the
+// reference's apply_epilogue order, src/kernels/fused_epilogue.cuh:11-16) and stores straight from the registers:
+// 4-byte pixel pairs (lane pairs exchange halves by DPP) or 2-byte values. split > 1: FP32 partials
 // partial[z][NCHW] over the z-th range of channel slices [floor(S*z/split), floor(S*(z+1)/split)), the partition of
 // src/kernels/tensor_core_mma.cu:112-115, reduced by splitk_reduce.hip.
 // Grid: units (split range, image, slab, 32-filter block); XCD x (slot mod 8) takes a contiguous range of units, with
@@ -120,7 +118,6 @@ struct SlabShape {
   static constexpr int R = CHP / 256;                   // 4-byte load instructions per channel
   static constexpr int KA = ACT / 256 / NW;             // 4-byte load instructions per wave per slice
   static constexpr int KR = (CS * NR * (P - 1) + NT - 1) / NT;  // 2-byte form: elements per thread per slice
-  static constexpr int KX = (CS * RB * (P - 1) / 8 + NT - 1) / NT;  // 16-byte form: chunks per thread per slice
   static constexpr int LDS = NST * (ACT + WST);         // [activation stages][weight stages]
   static constexpr int U = NST % 2 == 0 ? NST : 2 * NST;  // loop unroll: stage and register set are constants
   static_assert((16 * NBW) % P == 0, "a wave's rows are whole 16-position blocks");
@@ -137,14 +134,6 @@ __device__ __forceinline__ u32x4 rd16(unsigned a) { return *reinterpret_cast<con
 __device__ __forceinline__ u32x2 rd_tr(unsigned a) {
   const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4s*>(size_t(a)));
   return __builtin_bit_cast(u32x2, v);
-}
-
-// 4 bytes per lane straight into LDS at lds_base + 4 * lane (buffer_load_dword ... lds)
-__device__ __forceinline__ void dma4(v4i rsrc, unsigned lds_base, int voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(
-                   __builtin_amdgcn_readfirstlane(lds_base)),
-               "v"(voff), "s"(rsrc)
-               : "m0");
 }
 
 // segment slot swizzle of a channel: the 8 channels one half-wave reads (4 consecutive, and the 4 eight higher)
@@ -188,13 +177,6 @@ __device__ __forceinline__ void dma16s(v4i rsrc, unsigned lds_base, int voff, in
 }
 
 // register loads the compiler does not see as loads: valid after a counted wait_vmcnt (then touch_v)
-__device__ __forceinline__ u32x4 load16s(v4i rsrc, int voff, int soff) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
-               : "=v"(v)
-               : "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff)));
-  return v;
-}
 __device__ __forceinline__ uint32_t load2s(v4i rsrc, int voff, int soff) {
   uint32_t v;
   asm volatile("buffer_load_ushort %0, %1, %2, %3 offen"
@@ -217,9 +199,9 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
   }
 }
 
-// Activation load forms: kX16 = the whole image's 32-channel block by 16-byte register loads, written as pixel pairs;
-// kDma4 = 4-byte direct-to-LDS loads of every padded position; kReg2 = 2-byte register loads (odd rows).
-constexpr int kX16 = 0, kDma4 = 1, kReg2 = 2;
+// Activation load forms of the full and lean kernels: kDma4 = 4-byte direct-to-LDS loads of every padded position;
+// kReg2 = 2-byte register loads (odd rows, or x only 2-byte aligned).
+constexpr int kDma4 = 1, kReg2 = 2;
 
 // 4- and 2-byte buffer stores whose out-of-range offsets (kOut) the hardware drops: the epilogue masks lanes and
 // filters through the offset instead of the execution mask
@@ -243,7 +225,14 @@ __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uin
   constexpr int RW = 16 * NBW / P;
   (void)o0;
   auto column = [&](int j) __attribute__((always_inline)) {
-    if constexpr (PADS_LOADED) {
+    if constexpr (PADS_LOADED && P == 16) {
+      // a 16-position block is one row: the cross-block terms reach only column 0 (its left neighbour is padding)
+      // and column 15 (never stored), and the row shift already gives column 0 nothing; only the right neighbour of
+      // column W - 1, position W, has to be zeroed before the shift
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 a2 = (lane & 15) == g.W ? zero : acc[2][j];
+      return acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(a2);
+    } else if constexpr (PADS_LOADED) {
       f32x4 t0 = dpp4<kShr1>(acc[0][j]), t2 = dpp4<kShl1>(acc[2][j]);
       if (j > 0) t0 += dpp4<kShl15>(acc[0][j - 1]);
       if (j + 1 < NBW) t2 += dpp4<kShr15>(acc[2][j + 1]);
@@ -328,9 +317,9 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
   constexpr int CS = Sh::CS, NW = Sh::NW, NT = Sh::NT, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G;
   constexpr int NBR = Sh::NBR, CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW;
   constexpr int WST = Sh::WST, CHP = Sh::CHP, ACT = Sh::ACT, KA = Sh::KA, R = Sh::R, U = Sh::U;
-  constexpr int KX = Sh::KX, KR = Sh::KR;
-  constexpr bool REG = MODE != kDma4;                   // activations through registers
-  constexpr int NL = MODE == kX16 ? KX : (MODE == kReg2 ? KR : 0);  // register loads per thread per slice
+  constexpr int KR = Sh::KR;
+  constexpr bool REG = MODE == kReg2;                   // activations through registers
+  constexpr int NL = REG ? KR : 0;                      // register loads per thread per slice
   constexpr int NI = KBW + (MODE == kDma4 ? KA : NL);   // loads per wave per slice
   constexpr int WOFF = NST * ACT;                       // LDS: [activation stages][weight stages]
   static_assert(NST * NI < 64, "loads in flight fit the vmcnt counter");
@@ -389,31 +378,13 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
       a_voff[v] = (row < NR && ih >= 0 && ih < g.H && col < g.W) ? (ih * g.W + col) * 2 : kOut;
     }
   }
-  // ---- activations, register forms: the thread's elements of the slice (fixed across slices) ----
-  // kX16: chunk c = k * NT + tid = halves 8c .. 8c+7 of the image's contiguous 32-channel block, as 4 pixel pairs
-  // kReg2: element e = k * NT + tid of (channel, input row of the slab, column)
+  // ---- activations, register form: element e = k * NT + tid of (channel, input row of the slab, column), the
+  // thread's elements fixed across slices ----
   int r_voff[NL > 0 ? NL : 1];
-  unsigned r_dst[NL > 0 ? NL : 1][MODE == kX16 ? 4 : 1];
-  int r_lim[NL > 0 ? NL : 1];  // element index (kX16: half index of the pair) compared against the slice's channels
-  u32x4 r_v16[MODE == kX16 ? NL : 1];
-  uint32_t r_v2[MODE == kReg2 ? NL : 1];
-  const int blk = CS * g.HW;  // halves of the block (kX16)
-  if constexpr (MODE == kX16) {
-#pragma unroll
-    for (int k = 0; k < NL; ++k) {
-      const int c = k * NT + tid;
-      r_voff[k] = 8 * c < blk ? 16 * c : kOut;
-      r_lim[k] = 8 * c;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int e = min(8 * c + 2 * q, blk - 2);
-        const int ch = fdiv(e, g.HW, g.inv_hw), px = e - ch * g.HW;
-        const int row = fdiv(px, g.W, g.inv_w), col = px - row * g.W;
-        const int pos = (row + 1) * P + col;
-        r_dst[k][q] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
-      }
-    }
-  } else if constexpr (MODE == kReg2) {
+  unsigned r_dst[NL > 0 ? NL : 1];
+  int r_lim[NL > 0 ? NL : 1];  // the element's channel, compared against the slice's channels
+  uint32_t r_v2[NL > 0 ? NL : 1];
+  if constexpr (REG) {
     const int ih_lo = max(oh0 - 1, 0), ih_hi = min(oh0 + RB + 1, g.H);
     const int per_ch = (ih_hi - ih_lo) * g.W;
 #pragma unroll
@@ -422,13 +393,12 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
       const int pos = (ih_lo - oh0 + 1 + rr) * P + col;
       r_voff[k] = ch < CS ? (ch * g.HW + (ih_lo + rr) * g.W + col) * 2 : kOut;
       r_lim[k] = ch < CS ? ch : (1 << 24);
-      r_dst[k][0] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
+      r_dst[k] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
     }
   }
 
-  // the next slice in order: activations (register forms: into registers v16 / v2, written one step later)...
-  auto issue_act = [&](int st, u32x4 (&v16)[MODE == kX16 ? NL : 1], uint32_t (&v2)[MODE == kReg2 ? NL : 1])
-                       __attribute__((always_inline)) {
+  // the next slice in order: activations (register form: into registers v2, written one step later)...
+  auto issue_act = [&](int st, uint32_t (&v2)[NL > 0 ? NL : 1]) __attribute__((always_inline)) {
     if constexpr (MODE == kDma4) {
       const unsigned ab = lds0 + unsigned(st * ACT + wave * KA * 256);
 #pragma unroll
@@ -437,10 +407,6 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
         dma4s(xr, ab + unsigned(i * 256), a_c0 + 8 * wave + i / R < g.C ? a_voff[(i % R) + R * ((i / R) & 3)] : kOut,
               soff);
       }
-    } else if constexpr (MODE == kX16) {
-      const int soff = (b * g.C + a_c0) * g.HW * 2;
-#pragma unroll
-      for (int k = 0; k < NL; ++k) v16[k] = load16s(xr, r_voff[k], soff);
     } else {
       const int soff = (b * g.C + a_c0) * g.HW * 2;
 #pragma unroll
@@ -464,44 +430,18 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
     w_soff += CS * 18;
     w_rem -= CS;
   };
-  // register forms: activations loaded into registers (set v) by an earlier issue, for the slice with channel base
-  // c0, written into stage st (the caller has waited for them)
-  typedef __attribute__((address_space(3))) uint32_t lds_u32;
-  auto write_regs = [&](int st, int c0, const u32x4 (&v16)[MODE == kX16 ? NL : 1],
-                        const uint32_t (&v2)[MODE == kReg2 ? NL : 1]) __attribute__((always_inline)) {
-    if constexpr (MODE == kX16) {
-      const int lim = (g.C - c0) * g.HW;  // halves of the block inside C
-      if (lim >= blk) {
-#pragma unroll
-        for (int k = 0; k < NL; ++k) {
-          // chunk slots wholly inside the block write unconditionally; the others only where the chunk exists
-          if ((k + 1) * NT * 8 <= blk || r_voff[k] != kOut) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) *reinterpret_cast<lds_u32*>(size_t(r_dst[k][q] + unsigned(st * ACT))) = v16[k][q];
-          }
-        }
-      } else {  // the slice runs past C: pairs of channels >= C are written as zeros
-#pragma unroll
-        for (int k = 0; k < NL; ++k) {
-          if (r_voff[k] != kOut) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              *reinterpret_cast<lds_u32*>(size_t(r_dst[k][q] + unsigned(st * ACT))) = r_lim[k] + 2 * q < lim ? v16[k][q] : 0u;
-          }
-        }
-      }
-    } else if constexpr (MODE == kReg2) {
+  // register form: activations loaded into registers by an earlier issue, for the slice with channel base c0, written
+  // into stage st (the caller has waited for them); elements of channels past the slice are not written
+  auto write_regs = [&](int st, const uint32_t (&v2)[NL > 0 ? NL : 1]) __attribute__((always_inline)) {
+    if constexpr (REG) {
 #pragma unroll
       for (int k = 0; k < NL; ++k)
-        if (r_lim[k] < CS) *reinterpret_cast<lds_h*>(size_t(r_dst[k][0] + unsigned(st * ACT))) = uint16_t(v2[k]);
+        if (r_lim[k] < CS) *reinterpret_cast<lds_h*>(size_t(r_dst[k] + unsigned(st * ACT))) = uint16_t(v2[k]);
     }
   };
   auto touch_regs = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int k = 0; k < NL; ++k) {
-      if constexpr (MODE == kX16) touch_v(r_v16[k]);
-      if constexpr (MODE == kReg2) touch_v(r_v2[k]);
-    }
+    for (int k = 0; k < NL; ++k) touch_v(r_v2[k]);
   };
 
   // ---- fragment addresses (stage 0; the stage offset is the instruction's immediate offset) ----
@@ -562,13 +502,12 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
     __syncthreads();
   }
   {
-    u32x4 p16[NST - 1][MODE == kX16 ? NL : 1];
-    uint32_t p2[NST - 1][MODE == kReg2 ? NL : 1];
+    uint32_t p2[NST - 1][NL > 0 ? NL : 1];
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       if (st < ns) {
-        if (st + 1 < NST) issue_act(st, p16[st], p2[st]);
-        else issue_act(st, r_v16, r_v2);  // written in step 0
+        if (st + 1 < NST) issue_act(st, p2[st]);
+        else issue_act(st, r_v2);  // written in step 0
         issue_w(st);
       }
     }
@@ -578,13 +517,10 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
       for (int st = 0; st + 1 < NST; ++st) {
         if (st < ns) {
           // issued after slice st's activations: its weights and the slices st+1 .. min(NST, ns)-1
-          wait_vm_upto<KBW + (NST - 1) * Sh::KX + (NST - 1) * KBW + 8>(KBW + (min(NST, ns) - 1 - st) * NI);
+          wait_vm_upto<KBW + (NST - 1) * NI>(KBW + (min(NST, ns) - 1 - st) * NI);
 #pragma unroll
-          for (int k = 0; k < NL; ++k) {
-            if constexpr (MODE == kX16) touch_v(p16[st][k]);
-            if constexpr (MODE == kReg2) touch_v(p2[st][k]);
-          }
-          write_regs(st, (s_beg + st) * CS, p16[st], p2[st]);
+          for (int k = 0; k < NL; ++k) touch_v(p2[st][k]);
+          write_regs(st, p2[st]);
         }
       }
     }
@@ -647,11 +583,11 @@ __global__ __launch_bounds__(256, 1) void slab_kernel(const uint16_t* __restrict
     if (more) transpose_a(nxt, 6, 9);
     __builtin_amdgcn_sched_barrier(0);
     mfma_tap(cur, 5);
-    if (wr_now) write_regs(st_write, (s_beg + i + NST - 1) * CS, r_v16, r_v2);
+    if (wr_now) write_regs(st_write, r_v2);
     __builtin_amdgcn_sched_barrier(0);
     mfma_tap(cur, 6);
     if (ld_now) {
-      issue_act(st_load, r_v16, r_v2);
+      issue_act(st_load, r_v2);
       issue_w(st_load);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1121,7 +1057,7 @@ struct SlabCfg {
 constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3, kFull}, {16, 7, 2, kFull}, {16, 4, 3, kFull}, {8, 2, 3, kFull},
                                  {8, 4, 3, kFull},  {32, 4, 3, kFull}, {16, 7, 2, kLean}, {16, 4, 2, kLean},
                                  {8, 2, 2, kLean},  {8, 4, 2, kLean},  {32, 4, 2, kLean}, {16, 7, 3, kLean},
-                                 {16, 7, 3, kPipe}, {16, 4, 3, kPipe}};
+                                 {16, 7, 3, kPipe}};
 constexpr int kSlabN = int(sizeof(kSlabCfgs) / sizeof(kSlabCfgs[0]));
 
 template <int I>
@@ -1200,10 +1136,8 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   if (!dispatch(cfg, bf, kDma4, &fn, &si, std::make_integer_sequence<int, kSlabN>{})) return GIE_HIP_EINVAL;
   if (gg->in_w + 1 > si.P) return GIE_HIP_EUNSUPPORTED;
   const int bands = (gg->in_h + si.RB - 1) / si.RB;
-  // activation load form: even rows take 4-byte loads (16-byte register loads when the slab is the whole image and
-  // x is 16-byte aligned); odd rows or a 2-byte aligned x take 2-byte loads
-  // (the 16-byte register form of whole-image slabs measured slower than the direct loads on config 2: 16.0 vs
-  // 14.9 us, so even rows always take the direct form)
+  // activation load form: even rows of a 4-byte aligned x take direct loads; odd rows or a 2-byte aligned x take
+  // 2-byte register loads (full form only)
   const bool even = gg->in_w % 2 == 0 && !(reinterpret_cast<uintptr_t>(x) & 3u);
   SlabFn alt = nullptr;
   if (!even) {
@@ -1296,7 +1230,7 @@ std::mutex g_scratch_mu;
 int raise_lds_limits() {
   for (int cfg = 0; cfg < kSlabN; ++cfg)
     for (int bf = 0; bf < 2; ++bf)
-      for (int mode : {kX16, kDma4, kReg2}) {
+      for (int mode : {kDma4, kReg2}) {
         SlabFn fn = nullptr;
         SlabShapeInfo si{};
         if (!dispatch(cfg, bf != 0, mode, &fn, &si, std::make_integer_sequence<int, kSlabN>{}) || fn == nullptr ||
