@@ -234,8 +234,9 @@ __global__ __launch_bounds__(kPwNT, 2) void pw_kernel(const uint16_t* __restrict
 // 256 filters x all C input channels in VGPRs for its whole life and streams one contiguous range of 64-pixel
 // blocks of the flattened B*H*W pixel axis through a four-stage LDS ring:
 //   * the weights come in once per workgroup: 256 filters x C by LDS-DMA into the LDS the ring and the output
-//     tiles use later, laid out [k-step][k-half][filter] in 16-byte units so every wave reads its B operands
-//     (filters 64*(w%4) .. +63, W[o][16j + 8*(lane/32) ..]) with conflict-free ds_read_b128;
+//     tiles use later, each filter's OIHW row as 16-byte slots permuted by the filter index (kc ^ (f % RC)), so the
+//     loads read whole rows and every wave's B-operand reads (filters 64*(w%4) .. +63, W[o][16j + 8*(lane/32) ..])
+//     have at most two-way bank conflicts;
 //   * block i = X[b][0 .. C)[p .. p+63] as two [channel][32 pixels] halves with 64-byte rows (16-byte chunks by
 //     LDS-DMA; a block may straddle two images, each 8-pixel chunk is addressed on its own, H*W % 8 == 0);
 //   * wave w takes pixel half w/4 against its 64 filters: A fragments by ds_read_b64_tr_b16 (rows k..k+3 of a
@@ -401,13 +402,15 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
 
   // ---- prologue 1: block 0 into stage 0, the weights into the rest of LDS, the lane's bias values ----
   issue(0, 0, base_of(0));
+  // weights: [256 filters][RC 16-byte slots], filter f's chunk kc (channels 8kc .. 8kc+7) in slot kc ^ (f % RC), so
+  // a load instruction covers two whole OIHW rows (1 KiB contiguous) and the 32 filters of a B-operand read spread
+  // over the banks
+  constexpr int RC = 2 * KS;  // 16-byte chunks per filter row
 #pragma unroll
   for (int t = 0; t < WL; ++t) {
-    // 16-byte unit e = 64*(wave + 8t) + lane of the weight area: filter e % 256, k-half (e / 256) % 2, k-step
-    // e / 512 (the layout the B-operand reads below want)
-    const int e = 64 * (wave + kSwNW * t) + lane;
-    const int o = o0 + (e & 255), k = 16 * (e >> 9) + 8 * ((e >> 8) & 1);
-    dma16(wr, lds0 + W_OFF + (wave + kSwNW * t) * 1024, (o < g.O && k < g.C) ? (o * g.C + k) * 2 : kOut);
+    const int e = 64 * (wave + kSwNW * t) + lane, f = e / RC, kc = (e % RC) ^ (f % RC);
+    const int o = o0 + f;
+    dma16(wr, lds0 + W_OFF + (wave + kSwNW * t) * 1024, (o < g.O && 8 * kc < g.C) ? (o * g.C + 8 * kc) * 2 : kOut);
   }
   uint32_t braw[2];
   int o_lane[2];
@@ -425,8 +428,8 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
   for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      const unsigned e = unsigned(512 * j + 256 * (lane >> 5) + 64 * fg + 32 * nb + (lane & 31));
-      wf[nb][j] = lds_b128(lds0 + W_OFF + e * 16u);
+      const int f = 64 * fg + 32 * nb + (lane & 31), kc = 2 * j + (lane >> 5);
+      wf[nb][j] = lds_b128(lds0 + W_OFF + unsigned(f * RC + (kc ^ (f % RC))) * 16u);
     }
   stage_barrier();  // every wave holds its weights (lgkmcnt(0) in the barrier): the ring may overwrite them
 
