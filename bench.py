@@ -120,7 +120,7 @@ def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
 
 def repack_bytes(kernel: str, p):
     """HBM bytes the kernel's repack launch moves (reads of x/w plus writes of the repacked copies), or None for a
-    family that has no repack launch (slab, pw, stem and narrow read NCHW x and OIHW w directly)."""
+    family that has no repack launch (slab, stack, pw, stem and narrow read NCHW x and OIHW w directly)."""
     e = p.esize
     nx, nw = float(np.prod(p.x_shape())), float(np.prod(p.w_shape()))
     taps = p.kernel_h * p.kernel_w
@@ -245,6 +245,7 @@ def dominant_kernel(registry_name: str) -> str:
              ("halo_", "halo_kernel (halo-tiled MFMA implicit GEMM, conv_halo.hip)"),
              ("stem_", "stem_kernel (7x7 stride-2 stem straight from NCHW, conv_stem.hip)"),
              ("narrow_", "narrow_kernel (3x3, whole reduction per workgroup, conv_narrow.hip)"),
+             ("stack_", "stack_kernel (3x3 MFMA convolution of small images stacked per workgroup, conv_stack.hip)"),
              ("implicit_gemm_fp32_", "f32_kernel (FP32 MFMA convolution, conv_f32.hip)"),
              ("mfma_tf32_", "f32_kernel (TF32 MFMA convolution, conv_f32.hip)")]
     for stem, fn in stems:

@@ -39,7 +39,7 @@
 #include <atomic>
 #include <mutex>
 
-#include "lds_pipe.h"
+#include "slab_common.h"
 
 namespace gie_hip {
 namespace {
@@ -63,10 +63,6 @@ struct SlabGeom {
   unsigned mg[3];  // n / rad[k] = (umulhi(n, mg[k]) + n) >> sh[k] for n < 2^30
   int sh[3];
 };
-
-__device__ __forceinline__ int magic_div(int n, unsigned mg, int sh) {
-  return int((__umulhi(unsigned(n), mg) + unsigned(n)) >> sh);
-}
 
 struct SlabUnit {
   int b, z, ob, band;
@@ -127,90 +123,9 @@ struct SlabShape {
   static_assert(LDS <= kLdsLimit, "LDS budget");
 };
 
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) u32x4 lds_v4;
-typedef __attribute__((address_space(3))) uint16_t lds_h;
-__device__ __forceinline__ u32x4 rd16(unsigned a) { return *reinterpret_cast<const lds_v4*>(size_t(a)); }
-__device__ __forceinline__ u32x2 rd_tr(unsigned a) {
-  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4s*>(size_t(a)));
-  return __builtin_bit_cast(u32x2, v);
-}
-
-// segment slot swizzle of a channel: the 8 channels one half-wave reads (4 consecutive, and the 4 eight higher)
-// land on 8 distinct 32-byte bank groups
-__device__ __forceinline__ int seg_swz(int ch) { return (ch & 3) | (((ch >> 3) & 1) << 2); }
-
-// half a of the 144-byte weight run (8 channels x 9 taps) in the low 16 bits, half b in the high 16 bits
-__device__ __forceinline__ uint32_t pick2(const uint32_t (&d)[36], int a, int b) {
-  const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;          // bytes of S1 = d[a >> 1]
-  const uint32_t hi = (b & 1) ? 0x07060000u : 0x05040000u;  // bytes of S0 = d[b >> 1]
-  return __builtin_amdgcn_perm(d[b >> 1], d[a >> 1], lo | hi);
-}
-
-// lane i of each 16-lane row takes lane i + k (row_shl) or i - k (row_shr); lanes without a source read 0
-template <int CTRL>
-__device__ __forceinline__ f32x4 dpp4(const f32x4& v) {
-  f32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), CTRL, 0xf, 0xf, true));
-  return r;
-}
-constexpr int kShl1 = 0x101, kShl15 = 0x10F, kShr1 = 0x111, kShr15 = 0x11F;
-
-// direct-to-LDS loads whose per-slice advance travels in the scalar offset, so the per-lane offsets are set up once
-// (the resource is wave-uniform by construction; readfirstlane states it for the compiler)
-__device__ __forceinline__ v4i uniform4(v4i r) {
-  return v4i{__builtin_amdgcn_readfirstlane(r.x), __builtin_amdgcn_readfirstlane(r.y),
-             __builtin_amdgcn_readfirstlane(r.z), __builtin_amdgcn_readfirstlane(r.w)};
-}
-__device__ __forceinline__ void dma4s(v4i rsrc, unsigned lds_base, int voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(
-                   __builtin_amdgcn_readfirstlane(lds_base)),
-               "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff))
-               : "m0");
-}
-__device__ __forceinline__ void dma16s(v4i rsrc, unsigned lds_base, int voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(
-                   __builtin_amdgcn_readfirstlane(lds_base)),
-               "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff))
-               : "m0");
-}
-
-// register loads the compiler does not see as loads: valid after a counted wait_vmcnt (then touch_v)
-__device__ __forceinline__ uint32_t load2s(v4i rsrc, int voff, int soff) {
-  uint32_t v;
-  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen"
-               : "=v"(v)
-               : "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff)));
-  return v;
-}
-
-// s_waitcnt vmcnt(n) for a wave-uniform n < 64 known only at run time (prologue bookkeeping)
-template <int N>
-__device__ __forceinline__ void wait_vm_upto(int n) {
-  if constexpr (N > 0) {
-    if (n >= N) {
-      wait_vm<N>();
-      return;
-    }
-    wait_vm_upto<N - 1>(n);
-  } else {
-    wait_vm<0>();
-  }
-}
-
 // Activation load forms of the full and lean kernels: kDma4 = 4-byte direct-to-LDS loads of every padded position;
 // kReg2 = 2-byte register loads (odd rows, or x only 2-byte aligned).
 constexpr int kDma4 = 1, kReg2 = 2;
-
-// 4- and 2-byte buffer stores whose out-of-range offsets (kOut) the hardware drops: the epilogue masks lanes and
-// filters through the offset instead of the execution mask
-__device__ __forceinline__ void store4(v4i rsrc, int voff, uint32_t v) {
-  asm volatile("buffer_store_dword %0, %1, %2, 0 offen" ::"v"(v), "v"(voff), "s"(uniform4(rsrc)) : "memory");
-}
-__device__ __forceinline__ void store2(v4i rsrc, int voff, uint32_t v) {
-  asm volatile("buffer_store_short %0, %1, %2, 0 offen" ::"v"(v), "v"(voff), "s"(uniform4(rsrc)) : "memory");
-}
 
 // Epilogue of one unit, shared by the slab kernels: tap-column shifts (DPP), then split 1: bias + ReLU + one rounding
 // and pixel-pair (or 2-byte) stores straight from the accumulators; split > 1: FP32 partials. One loop per store
@@ -840,11 +755,6 @@ struct PipeSched {
   static constexpr int perm_slot(int p) { return PB + p * (NM - PB) / 36; }
   static constexpr int load_slot(int q, int ni) { return q * NM / ni; }
 };
-
-template <typename F, int... K>
-__device__ __forceinline__ void for_seq(F&& f, std::integer_sequence<int, K...>) {
-  (f(std::integral_constant<int, K>{}), ...);
-}
 
 template <typename E, int P, int NBW, int NST>
 __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __restrict__ x,

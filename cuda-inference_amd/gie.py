@@ -78,6 +78,10 @@ class GieSlabConfig(ctypes.Structure):
                                             "form", "threads", "lds_bytes", "version")]
 
 
+class GieStackConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "rows", "pitch", "tile_k", "threads", "lds_bytes", "version")]
+
+
 class GieDeviceModel(ctypes.Structure):
     _fields_ = [("cus", ctypes.c_int), ("mfma_tflops", ctypes.c_double), ("fp32_tflops", ctypes.c_double),
                 ("hbm_gbs", ctypes.c_double), ("launch_us", ctypes.c_double), ("lds_per_workgroup", ctypes.c_size_t)]
@@ -205,6 +209,10 @@ _HIP = {
     "gie_hip_conv_slab": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_conv_slab_noalloc": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_slab_scratch_floats": ([], ctypes.c_longlong),
+    "gie_hip_stack_config_count": ([], _i),
+    "gie_hip_stack_config_get": ([_i, ctypes.POINTER(GieStackConfig)], _i),
+    "gie_hip_stack_check": ([_i, _GP, _ip, _ip], _i),
+    "gie_hip_conv_stack": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_f32_config_count": ([], _i),
     "gie_hip_f32_config_tile_m": ([_i], _i),
     "gie_hip_f32_check": ([_i, _GP, _vp], _i),

@@ -30,6 +30,11 @@
  *                                    layers, fused: one launch straight from NCHW x / OIHW w
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,297-324
  *   gie_hip_slab_config_*            the registered tile table             src/kernels/tensor_core_mma.cu:370-388
+ *   gie_hip_conv_stack, _stack_check both transposes + tcmma_kernel (split-K partials included) for 3x3 stride-1
+ *                                    layers with small images and a long reduction, fused: one launch straight from
+ *                                    NCHW x / OIHW w, images of a group stacked in one plane
+ *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,297-324
+ *   gie_hip_stack_config_*           the registered tile table             src/kernels/tensor_core_mma.cu:370-388
  *   gie_hip_conv_f32, _f32_check     implicit_gemm_kernel<<<>>> launch (FP32) and the TF32 path
  *                                                                         src/kernels/implicit_gemm.cu:47-189,204-214
  *   gie_hip_f32_config_*             the registered FP32 tile table        src/kernels/implicit_gemm.cu:218-268
@@ -257,6 +262,32 @@ int gie_hip_conv_slab(int config, int dtype, const gie_conv_geom* g, const void*
 int gie_hip_conv_slab_noalloc(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w,
                               const void* bias, void* y, int split, void* stream);
 long long gie_hip_slab_scratch_floats(void);
+
+/* One registered stack configuration: tile_m (32) output channels x `rows` stack rows (a group of images of in_h
+   rows each plus one zero separator row per image, laid out `pitch` positions per row, in_w + 1 <= pitch), channel
+   slices of tile_k. */
+typedef struct gie_stack_config {
+  int tile_m, rows, pitch, tile_k;
+  int threads;
+  int lds_bytes;
+  int version;
+} gie_stack_config;
+
+int gie_hip_stack_config_count(void);
+int gie_hip_stack_config_get(int index, gie_stack_config* out);
+/* 0 when configuration `config` runs geometry g (3x3 filter, stride 1, padding 1, in_channels % 32 == 0,
+   in_w + 1 <= pitch, in_h + 1 <= rows, sizes within 32-bit offsets): LDS bytes per workgroup in *lds_bytes, images
+   stacked per workgroup in *images_per_unit (either may be NULL). */
+int gie_hip_stack_check(int config, const gie_conv_geom* g, int* lds_bytes, int* images_per_unit);
+
+/* Stacked-image convolution on MFMA 16x16x32 (FP32 accumulation) straight from the caller's NCHW x and OIHW w, for
+   3x3 layers with small images and a long reduction: each workgroup owns 32 output channels x a group of images
+   stacked into one tall zero-separated plane x one range of channel slices. x 4-byte aligned and w 16-byte aligned
+   (GIE_HIP_EUNSUPPORTED otherwise); y and bias 2-byte aligned. split == 1: y (NCHW) = round(relu?(acc + bias)), one
+   rounding. split > 1: partial[z][NCHW index] = FP32 sum over the channel slices [floor(S*z/split),
+   floor(S*(z+1)/split)), S = in_channels / 32; reduce with gie_hip_splitk_reduce. 1 <= split <= S. */
+int gie_hip_conv_stack(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w,
+                       const void* bias, void* y, float* partial, int split, void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
    dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */

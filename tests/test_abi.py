@@ -204,3 +204,45 @@ def test_slab_geometry_check_on_host():
               gie.Problem(1, 64, 8, 40, 32, 3, 3, 1, 1, 1, 1, precision="fp16")):
         for i in range(n):
             assert h.gie_hip_slab_check(i, ctypes.byref(p.geom(p.in_channels)), None) != 0
+
+
+def test_stack_configuration_table_and_geometry_on_host():
+    """The stack configurations answer their table query consistently, their registry entries exist for both
+    precisions and every split factor, gie_hip_stack_check (host arithmetic) accepts the GPU stack tests' shapes with
+    the images per unit the stack holds, and refuses what the kernel cannot run."""
+    h = gie.hip()
+    n = h.gie_hip_stack_config_count()
+    assert n >= 1
+    for i in range(n):
+        c = gie.GieStackConfig()
+        assert h.gie_hip_stack_config_get(i, ctypes.byref(c)) == 0, i
+        assert c.tile_m == 32 and c.tile_k == 32 and c.pitch == 8 and c.threads == 256
+        assert (c.rows // 2) * c.pitch % 16 == 0 and 0 < c.lds_bytes <= 160 * 1024
+    assert h.gie_hip_stack_config_get(n, ctypes.byref(gie.GieStackConfig())) != 0
+    names = gie.registry()
+    for prec in ("fp16", "bf16"):
+        for sk in (1, 2, 4, 8):
+            assert any(k.startswith(f"stack_{prec}_3x3_") and k.endswith(f"_sk{sk}") for k in names), (prec, sk)
+    rows = []
+    for i in range(n):
+        c = gie.GieStackConfig()
+        h.gie_hip_stack_config_get(i, ctypes.byref(c))
+        rows.append(c.rows)
+    for B, C, H, W, K in [(8, 512, 7, 7, 64), (3, 64, 7, 7, 40), (5, 96, 6, 5, 20), (2, 32, 4, 4, 8),
+                          (16, 64, 3, 7, 32), (4, 128, 7, 1, 16), (2, 64, 15, 7, 32), (6, 160, 5, 6, 48),
+                          (1, 96, 2, 3, 33), (8, 512, 7, 7, 512)]:
+        p = gie.Problem(B, C, H, W, K, 3, 3, 1, 1, 1, 1, precision="bf16")
+        ok = 0
+        for i in range(n):
+            lds, ni = ctypes.c_int(0), ctypes.c_int(0)
+            if h.gie_hip_stack_check(i, ctypes.byref(p.geom(C)), ctypes.byref(lds), ctypes.byref(ni)) == 0:
+                assert ni.value == min(rows[i] // (H + 1), B), (i, B, H)
+                ok += 1
+        assert ok > 0, (B, C, H, W, K)
+    for p in (gie.Problem(2, 64, 7, 7, 64, 5, 5, 1, 1, 2, 2, precision="fp16"),   # 5x5
+              gie.Problem(2, 64, 7, 7, 64, 3, 3, 2, 2, 1, 1, precision="fp16"),   # stride 2
+              gie.Problem(2, 72, 7, 7, 64, 3, 3, 1, 1, 1, 1, precision="fp16"),   # C % 32 != 0
+              gie.Problem(2, 64, 7, 8, 64, 3, 3, 1, 1, 1, 1, precision="fp16"),   # rows wider than the pitch allows
+              gie.Problem(1, 64, 40, 7, 32, 3, 3, 1, 1, 1, 1, precision="fp16")):  # images taller than every stack
+        for i in range(n):
+            assert h.gie_hip_stack_check(i, ctypes.byref(p.geom(p.in_channels)), None, None) != 0

@@ -112,12 +112,3 @@ def test_bench_config5_full_size():
     gates = b.gates(y)
     assert m.passed(), f"{k}: {m.summary()}"
     assert gates["rel_l2"] <= 1e-3 and gates["max_abs"] <= 2e-2, f"{k}: {gates}"
-
-
-def test_dispatcher_routes_config5_to_the_narrow_entry():
-    """The cost model alone (no tuning) picks the narrow entry for BASELINE config 5."""
-    c = dict(BENCH_CONFIGS["c5_bf16_3x3_splitk"])
-    prec = c.pop("precision")
-    p = gie.Problem(**c, precision=prec, has_bias=True, relu=True)
-    k, src, _ = gie.select(p)
-    assert k == "narrow_bf16_3x3_32x32x16_k8w" and src == "cost_model", (k, src)
