@@ -80,7 +80,7 @@ __device__ __forceinline__ u32x4 load16s(v4i rsrc, int voff, int soff) {
 }
 __device__ __forceinline__ void wr16(unsigned a, u32x4 v) { *reinterpret_cast<lds_v4*>(size_t(a)) = v; }
 
-template <int P, int NBW>
+template <int P, int NBW, int KH>
 struct StackShape {
   static constexpr int RW = 16 * NBW / P;               // stack rows per wave
   static constexpr int RB = 2 * RW;                     // stack rows per unit
@@ -99,7 +99,10 @@ struct StackShape {
   static constexpr int CHP = (NR * P * 2 + 224 + 255) / 256 * 256;
   static constexpr int ACT = CS * CHP;
   static constexpr int KR = (CS * RB + NT - 1) / NT;    // activation rows (items) per thread per slice
-  static constexpr int LDS = 2 * (ACT + WST);           // [2 activation stages][2 weight stages]
+  static constexpr int LDSH = 2 * (ACT + WST);          // one channel half: [2 activation stages][2 weight stages]
+  static constexpr int LDS = KH * LDSH;
+  static_assert(KH == 1 || KH == 2, "one or two channel halves");
+  static_assert(KH == 1 || 4 * 64 * 3 * NBW * 16 <= LDSH, "a half's accumulators fit its LDS for the combine");
   static_assert(P == 8, "rows of one 16-byte chunk (in_w <= 7), 16-position blocks of whole rows");
   static_assert((16 * NBW) % P == 0, "a wave's rows are whole 16-position blocks");
   static_assert(ACT + 16 * NBR < 65536 && WST + 256 < 65536, "stage offsets fit the LDS offset field");
@@ -113,7 +116,7 @@ __device__ __forceinline__ unsigned plane_of(int ch, int chp) { return unsigned(
 // register loads (into the same registers) after them, weight loads spread over the step
 template <int P, int NBW>
 struct StackSched {
-  using Sh = StackShape<P, NBW>;
+  using Sh = StackShape<P, NBW, 1>;
   static constexpr int NM = 9 * NBW;
   static constexpr int NRD = 9 + 2 * Sh::NBR;
   static constexpr int NRS = NRD < NM ? NRD : NM;
@@ -126,11 +129,11 @@ struct StackSched {
   static constexpr int wld_slot(int q) { return q * NM / Sh::KBW; }
 };
 
-template <typename E, int P, int NBW>
-__global__ __launch_bounds__(256, 1) void stack_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+template <typename E, int P, int NBW, int KH>
+__global__ __launch_bounds__(256 * KH, 1) void stack_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                       const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
                                                       float* __restrict__ partial, StackGeom g) {
-  using Sh = StackShape<P, NBW>;
+  using Sh = StackShape<P, NBW, KH>;
   using Sc = StackSched<P, NBW>;
   constexpr int CS = Sh::CS, NW = Sh::NW, NT = Sh::NT, RW = Sh::RW, NR = Sh::NR, NBR = Sh::NBR;
   constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
@@ -141,8 +144,11 @@ __global__ __launch_bounds__(256, 1) void stack_kernel(const uint16_t* __restric
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   args_in_sgprs(x, w, bias, y, partial, g);
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // KH channel halves of 4 waves each: half h multiplies its share of the unit's slices in its own LDS stages, and
+  // the halves' accumulators are added through LDS before the epilogue
+  const int tid = threadIdx.x & 255, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & 3);
+  const int half = KH == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
   const int fh = wave & 1, wr = wave >> 1;
 
   // ---- unit: XCD (slot mod 8) takes units [xcd * per_xcd, ...) ----
@@ -152,15 +158,19 @@ __global__ __launch_bounds__(256, 1) void stack_kernel(const uint16_t* __restric
   const int q0 = magic_div(unit, g.mg_ig, g.sh_ig), ig = unit - q0 * g.n_ig;
   const int z = magic_div(q0, g.mg_ob, g.sh_ob), ob = q0 - z * g.n_ob;
   const int o0 = ob * kStTO, b0 = ig * g.NI;
-  int s_beg = 0, ns = g.S;
+  int s_beg = 0, nsu = g.S;  // the unit's slices
   if (g.split > 1) {
     s_beg = (g.S * z) / g.split;
-    ns = (g.S * (z + 1)) / g.split - s_beg;
+    nsu = (g.S * (z + 1)) / g.split - s_beg;
   }
+  // this half's slices: [s_beg + half * nsh, ...), ns of them real; every half runs nsh steps (the barriers are shared)
+  const int nsh = KH == 1 ? nsu : (nsu + 1) >> 1;
+  const int ns = KH == 1 ? nsu : max(0, min(nsh, nsu - half * nsh));
+  s_beg += half * nsh;
 
   const v4i xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
   const v4i x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: loads give zeros
-  const unsigned lds0 = lds_addr(lds);
+  const unsigned lds0 = lds_addr(lds) + unsigned(half * Sh::LDSH);
 
   // ---- load offsets first, so the first loads leave before the rest of the set-up ----
   // weights: block wave + NW * kb; lane slot u = (filter u / CPF, chunk u % CPF); per slice += CS * 18
@@ -361,9 +371,9 @@ __global__ __launch_bounds__(256, 1) void stack_kernel(const uint16_t* __restric
       __builtin_amdgcn_sched_barrier(0);
     }, std::make_integer_sequence<int, NM>{});
   };
-  for (int j = 0; j < ns; j += 2) {
+  for (int j = 0; j < nsh; j += 2) {
     step(j, I0{});
-    if (j + 1 < ns) step(j + 1, I1{});
+    if (j + 1 < nsh) step(j + 1, I1{});
   }
   // The last step's activation loads are never written anywhere, but the hardware still writes their registers when
   // the data arrives. The compiler sees an inline-assembly load as writing its registers at issue, so without the
@@ -373,6 +383,27 @@ __global__ __launch_bounds__(256, 1) void stack_kernel(const uint16_t* __restric
   touch_ra();
 #pragma unroll
   for (int i = 0; i < 4; ++i) touch_v(bbits[i]);
+  if constexpr (KH == 2) {
+    // half 1's accumulators through its own LDS (every wave has finished reading it: barrier), added by half 0 in a
+    // fixed order (half 0 + half 1), so the result is the same launch to launch
+    stage_barrier();
+    const unsigned cb = lds0 - unsigned(half * Sh::LDSH) + unsigned(Sh::LDSH) + unsigned((wave * 3 * NBW * 64 + lane) * 16);
+    if (half == 1) {
+#pragma unroll
+      for (int s2 = 0; s2 < 3; ++s2) {
+#pragma unroll
+        for (int j2 = 0; j2 < NBW; ++j2)
+          wr16(cb + unsigned((s2 * NBW + j2) * 64 * 16), __builtin_bit_cast(u32x4, acc[s2][j2]));
+      }
+    }
+    stage_barrier();
+    if (half == 1) return;
+#pragma unroll
+    for (int s2 = 0; s2 < 3; ++s2) {
+#pragma unroll
+      for (int j2 = 0; j2 < NBW; ++j2) acc[s2][j2] += __builtin_bit_cast(f32x4, rd16(cb + unsigned((s2 * NBW + j2) * 64 * 16)));
+    }
+  }
 
   // ---- epilogue: tap-column shifts, then FP32 partials (split > 1) or bias + ReLU + one rounding; positions outside
   // an image (padding columns, separator rows, images past the batch) and filters past O store to kOut (dropped).
@@ -433,29 +464,29 @@ __global__ __launch_bounds__(256, 1) void stack_kernel(const uint16_t* __restric
 
 // (16-position blocks per wave); pitch 8 for rows of up to 7 pixels
 struct StackCfg {
-  int P, NBW;
+  int P, NBW, KH;  // KH: channel halves per workgroup (4 waves each)
 };
-constexpr StackCfg kStackCfgs[] = {{8, 8}, {8, 4}, {8, 2}};
+constexpr StackCfg kStackCfgs[] = {{8, 8, 1}, {8, 4, 1}, {8, 2, 1}, {8, 4, 2}, {8, 2, 2}};
 constexpr int kStackN = int(sizeof(kStackCfgs) / sizeof(kStackCfgs[0]));
 
 typedef void (*StackFn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, StackGeom);
 
 template <int I>
 struct StCfgT {
-  static constexpr int P = kStackCfgs[I].P, NBW = kStackCfgs[I].NBW;
-  using Sh = StackShape<P, NBW>;
+  static constexpr int P = kStackCfgs[I].P, NBW = kStackCfgs[I].NBW, KH = kStackCfgs[I].KH;
+  using Sh = StackShape<P, NBW, KH>;
 };
 
 struct StackShapeInfo {
-  int P, RB, NT, LDS;
+  int P, RB, NT, LDS, KH;
   StackFn fp16, bf16;
 };
 
 template <int I>
 StackShapeInfo stack_shape_of() {
   using C = StCfgT<I>;
-  return StackShapeInfo{C::P, C::Sh::RB, C::Sh::NT, C::Sh::LDS, &stack_kernel<Fp16, C::P, C::NBW>,
-                        &stack_kernel<Bf16, C::P, C::NBW>};
+  return StackShapeInfo{C::P, C::Sh::RB, C::Sh::NT * C::KH, C::Sh::LDS, C::KH, &stack_kernel<Fp16, C::P, C::NBW, C::KH>,
+                        &stack_kernel<Bf16, C::P, C::NBW, C::KH>};
 }
 
 template <int... Is>
@@ -541,7 +572,8 @@ extern "C" int gie_hip_stack_config_get(int index, gie_stack_config* out) {
   out->tile_k = 32;
   out->threads = si.NT;
   out->lds_bytes = si.LDS;
-  out->version = 1;
+  out->halves = si.KH;
+  out->version = 2;
   return GIE_HIP_OK;
 }
 

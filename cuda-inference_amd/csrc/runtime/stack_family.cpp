@@ -186,12 +186,13 @@ void register_stack_family(std::vector<KernelDesc>& out) {
     KernelDesc k;
     k.name = std::string("stack_") + to_string(en.precision) + "_3x3_" + std::to_string(en.info.tile_m) + "x" +
              std::to_string(en.info.rows) + "r" + std::to_string(en.info.pitch) + "_k" +
-             std::to_string(en.info.tile_k) + "_sk" + std::to_string(en.split);
+             std::to_string(en.info.tile_k) + (en.info.halves > 1 ? "_h" + std::to_string(en.info.halves) : "") +
+             "_sk" + std::to_string(en.split);
     k.backend = Backend::kTensorCore;
     k.version = en.info.version;
     k.params = {{"block_m", en.info.tile_m}, {"rows", en.info.rows}, {"pitch", en.info.pitch},
                 {"block_k", en.info.tile_k}, {"kernel_h", 3}, {"kernel_w", 3}, {"stages", 2},
-                {"split_k", en.split}};
+                {"halves", en.info.halves}, {"split_k", en.split}};
     k.threads_per_block = en.info.threads;
     k.tile_m = en.info.tile_m;
     k.tile_n = en.info.rows * en.info.pitch;

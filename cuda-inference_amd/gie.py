@@ -79,7 +79,8 @@ class GieSlabConfig(ctypes.Structure):
 
 
 class GieStackConfig(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "rows", "pitch", "tile_k", "threads", "lds_bytes", "version")]
+    _fields_ = [(n, ctypes.c_int) for n in ("tile_m", "rows", "pitch", "tile_k", "threads", "lds_bytes", "halves",
+                                            "version")]
 
 
 class GieDeviceModel(ctypes.Structure):

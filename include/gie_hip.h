@@ -265,11 +265,13 @@ long long gie_hip_slab_scratch_floats(void);
 
 /* One registered stack configuration: tile_m (32) output channels x `rows` stack rows (a group of images of in_h
    rows each plus one zero separator row per image, laid out `pitch` positions per row, in_w + 1 <= pitch), channel
-   slices of tile_k. */
+   slices of tile_k; `halves` groups of 4 waves per workgroup each take part of the workgroup's slices (their
+   accumulators are added in LDS before the epilogue). */
 typedef struct gie_stack_config {
   int tile_m, rows, pitch, tile_k;
   int threads;
   int lds_bytes;
+  int halves;
   int version;
 } gie_stack_config;
 

@@ -216,7 +216,7 @@ def test_stack_configuration_table_and_geometry_on_host():
     for i in range(n):
         c = gie.GieStackConfig()
         assert h.gie_hip_stack_config_get(i, ctypes.byref(c)) == 0, i
-        assert c.tile_m == 32 and c.tile_k == 32 and c.pitch == 8 and c.threads == 256
+        assert c.tile_m == 32 and c.tile_k == 32 and c.pitch == 8 and c.halves in (1, 2) and c.threads == 256 * c.halves
         assert (c.rows // 2) * c.pitch % 16 == 0 and 0 < c.lds_bytes <= 160 * 1024
     assert h.gie_hip_stack_config_get(n, ctypes.byref(gie.GieStackConfig())) != 0
     names = gie.registry()
