@@ -260,12 +260,13 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
       acc0 = f32x16{0}, acc1 = f32x16{0};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        // halves h0..h7 = input columns 2*ow-4 .. 2*ow+3; the group is (h1, h3, h5, h7, h2, h4, h6, 0)
+        // halves h0..h7 = input columns 2*ow-4 .. 2*ow+3; the group is (h1, h3, h5, h7, h2, h4, h6, 0): one byte
+        // permute per dword (bytes 0-3 of the second operand, 4-7 of the first)
         u32x4 b;
-        b.x = (d[s][0] >> 16) | (d[s][1] & 0xffff0000u);  // kw 0, 2
-        b.y = (d[s][2] >> 16) | (d[s][3] & 0xffff0000u);  // kw 4, 6
-        b.z = (d[s][1] & 0xffffu) | (d[s][2] << 16);      // kw 1, 3
-        b.w = d[s][3] & 0xffffu;                          // kw 5, 0
+        b.x = __builtin_amdgcn_perm(d[s][1], d[s][0], 0x07060302u);  // kw 0, 2: high halves of dwords 0 and 1
+        b.y = __builtin_amdgcn_perm(d[s][3], d[s][2], 0x07060302u);  // kw 4, 6
+        b.z = __builtin_amdgcn_perm(d[s][2], d[s][1], 0x05040100u);  // kw 1, 3: low halves of dwords 1 and 2
+        b.w = d[s][3] & 0xffffu;                                      // kw 5, 0
         const int grp = 2 * s + hi;
         if (2 * s + 1 >= NG) {  // this step holds the bias group (and possibly the zero group)
           if (grp == NG) b = u32x4{one_bits<E>(), 0u, 0u, 0u};
