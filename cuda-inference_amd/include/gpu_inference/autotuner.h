@@ -65,11 +65,7 @@ class TuneCache {
   size_t size() const;
   const std::string& path() const { return path_; }
 
- private:
-  void load_locked() const;
-  void save_locked() const;
-  std::string path_;
-  mutable std::mutex mu_;
+  // one persisted winner (the file's per-key record)
   struct Entry {
     std::string kernel;
     int kernel_version = 0;
@@ -77,6 +73,12 @@ class TuneCache {
     double tuned_seconds = 0;
     std::string timestamp;
   };
+
+ private:
+  void load_locked() const;
+  void save_locked() const;
+  std::string path_;
+  mutable std::mutex mu_;
   mutable std::map<std::string, Entry> entries_;
   mutable std::string text_;  // file contents entries_ was parsed from
   mutable bool loaded_ = false;
