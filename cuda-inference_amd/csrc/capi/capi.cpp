@@ -301,6 +301,27 @@ int gie_plan_workspace_bytes(void* plan, size_t* bytes) {
   return guarded([&] { *bytes = plan_of(plan).workspace_bytes(); });
 }
 
+int gie_plan_lut_bytes(void* plan, size_t* bytes) {
+  return guarded([&] { *bytes = plan_of(plan).lut_bytes(); });
+}
+
+int gie_build_conv_lut(const gie_problem* p, int chunked, int32_t* out4, int64_t cap, int64_t* count) {
+  return guarded([&] {
+    GIE_REQUIRE(count != nullptr, StatusCode::kInvalidArgument, "null count");
+    const ConvProblem pr = to_problem(p);
+    const std::vector<LutEntry> t = chunked ? build_conv_lut_chunked(pr.p) : build_conv_lut(pr.p);
+    *count = int64_t(t.size());
+    if (out4 == nullptr) return;
+    GIE_REQUIRE(cap >= int64_t(t.size()), StatusCode::kInvalidArgument, "gather-table buffer too small");
+    for (size_t i = 0; i < t.size(); ++i) {
+      out4[4 * i + 0] = t[i].c_off;
+      out4[4 * i + 1] = t[i].r_off;
+      out4[4 * i + 2] = t[i].s_off;
+      out4[4 * i + 3] = t[i].pad_;
+    }
+  });
+}
+
 int gie_plan_kernel_name(void* plan, char* buf, size_t n) {
   return guarded([&] { copy_str(plan_of(plan).kernel().name, buf, n); });
 }
@@ -756,7 +777,54 @@ void garbage_launch(const LaunchArgs& la) {
                       "garbage fill");
 }
 void throwing_launch(const LaunchArgs&) { throw Error(StatusCode::kInternal, "deliberately failing test kernel"); }
+
+// gather-table probe: runs only 2x3 filters over 24 input channels (a shape no benchmark or parity case uses), so
+// the dispatcher never meets it elsewhere; its "convolution" copies the plan's device table into y
+bool lut_probe_shape(const ConvProblem& p, Precision want, std::string* why) {
+  if (p.precision == want && p.p.kernel_h == 2 && p.p.kernel_w == 3 && p.p.in_channels == 24) return true;
+  if (why) *why = "gather-table probe runs only 2x3 filters over 24 channels";
+  return false;
+}
+bool lut_probe_fp16(const ConvProblem& p, const DeviceInfo&, std::string* why) {
+  return lut_probe_shape(p, Precision::kFp16, why);
+}
+bool lut_probe_bf16(const ConvProblem& p, const DeviceInfo&, std::string* why) {
+  return lut_probe_shape(p, Precision::kBf16, why);
+}
+template <bool CHUNKED>
+void lut_probe_launch(const LaunchArgs& la) {
+  GIE_REQUIRE(la.plan_data != nullptr, StatusCode::kInternal, "needs_lut kernel launched without a gather table");
+  const int64_t k = la.problem->p.gemm_k();
+  const size_t table = size_t(CHUNKED ? k / 8 : k) * sizeof(LutEntry);
+  const size_t ybytes = size_t(la.problem->p.output_shape().numel()) * dtype_size(la.problem->dtype());
+  GIE_HIP_CHECK(hipMemcpyAsync(la.y, la.plan_data, table < ybytes ? table : ybytes, hipMemcpyDeviceToDevice,
+                               la.stream));
+}
 }  // namespace
+
+extern "C" int gie_testing_add_lut_probe_kernels(void) {
+  return guarded([&] {
+    std::vector<KernelDesc>& reg = kernel_registry_for_testing();
+    for (Precision p : {Precision::kFp16, Precision::kBf16}) {
+      for (bool chunked : {false, true}) {
+        const std::string name = std::string(chunked ? "test_lut_chunked_probe_" : "test_lut_probe_") + to_string(p);
+        if (find_kernel(name)) continue;
+        GIE_REQUIRE(reg.size() < reg.capacity(), StatusCode::kInternal, "registry capacity exhausted");
+        KernelDesc k;
+        k.name = name;
+        k.backend = Backend::kDirect;
+        k.threads_per_block = 64;
+        k.needs_lut = true;
+        k.lut_chunked = chunked;
+        k.efficiency_prior = 1e-6;
+        k.supports = p == Precision::kFp16 ? &lut_probe_fp16 : &lut_probe_bf16;
+        k.workspace_bytes = &no_workspace;
+        k.launch = chunked ? &lut_probe_launch<true> : &lut_probe_launch<false>;
+        reg.push_back(std::move(k));
+      }
+    }
+  });
+}
 
 extern "C" int gie_testing_add_faulty_kernels(int kind) {
   return guarded([&] {

@@ -1,8 +1,10 @@
 // ExecutionPlan (the role of src/runtime/execution_plan.cpp:40-138): everything that depends only on the problem
 // and the kernel is settled once in create() — capability check on the plan's device, workspace and persistent
-// sizes, per-plan kernel state, the operand footprints and a LaunchArgs record with every field but the pointers
-// and the stream — so execute() checks the caller's tensors against precomputed values and execute_unchecked()
-// copies that record, fills in five pointers and enqueues. Neither allocates or synchronizes.
+// sizes, per-plan kernel state, the gather table of a needs_lut kernel (built on the host, uploaded on a private
+// stream and waited for, so a capture running on another stream sees no foreign work), the operand footprints and
+// a LaunchArgs record with every field but the pointers and the stream — so execute() checks the caller's tensors
+// against precomputed values and execute_unchecked() copies that record, fills in five pointers and enqueues.
+// Neither allocates or synchronizes.
 #include "gpu_inference/execution_plan.h"
 
 #include <hip/hip_runtime.h>
@@ -38,6 +40,17 @@ bool ranges_meet(const void* a, size_t an, const void* b, size_t bn) {
 
 [[noreturn]] void bad_argument(const std::string& msg) { throw Error(StatusCode::kInvalidArgument, msg); }
 
+// Host-to-device copy that has completed on return, issued on a stream of its own (non-blocking, so it neither
+// waits for nor joins work on the legacy stream).
+void upload_now(void* dst, const void* src, size_t bytes) {
+  hipStream_t s = nullptr;
+  GIE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  const hipError_t copied = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
+  const hipError_t waited = copied == hipSuccess ? hipStreamSynchronize(s) : copied;
+  (void)hipStreamDestroy(s);
+  GIE_HIP_CHECK(waited);
+}
+
 // One operand against what the plan expects of it: a device pointer, the precision policy's storage type and the
 // problem's shape, in that order.
 void expect_operand(const char* role, const void* data, DataType dtype, const TensorShape& shape, DataType want_dtype,
@@ -71,6 +84,13 @@ std::shared_ptr<ExecutionPlan> ExecutionPlan::create(const ConvProblem& problem,
   pl.workspace_bytes_ = kernel.workspace_bytes(problem);
   pl.persistent_bytes_ = kernel.persistent_bytes ? kernel.persistent_bytes(problem) : 0;
   if (kernel.create_state) pl.state_ = kernel.create_state(problem);
+  if (kernel.needs_lut) {
+    const std::vector<LutEntry> table =
+        kernel.lut_chunked ? build_conv_lut_chunked(problem.p) : build_conv_lut(problem.p);
+    pl.lut_bytes_ = table.size() * sizeof(LutEntry);
+    pl.lut_ = DeviceBuffer(pl.lut_bytes_);
+    upload_now(pl.lut_.data(), table.data(), pl.lut_bytes_);
+  }
   const Conv2DParams& p = problem.p;
   const size_t es = dtype_size(problem.dtype());
   pl.x_bytes_ = size_t(p.input_shape().numel()) * es;
@@ -80,6 +100,7 @@ std::shared_ptr<ExecutionPlan> ExecutionPlan::create(const ConvProblem& problem,
   pl.proto_.problem = &pl.problem_;
   pl.proto_.dev = &dev;
   pl.proto_.plan_state = pl.state_.get();
+  pl.proto_.plan_data = pl.lut_.data();
   return plan;
 }
 

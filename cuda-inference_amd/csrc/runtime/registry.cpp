@@ -1,6 +1,9 @@
 // Kernel registry (the reference's registry.cpp contract: unique names, mandatory function pointers, stable
-// element addresses). The reference's per-(c,r,s) gather tables (src/kernels/conv_common.cu:39-50) have no
-// counterpart: every kernel here walks the filter taps with incremental offsets computed in registers.
+// element addresses) and the gather-table builders of the registry interface (the reference's
+// src/kernels/conv_common.cu:22-50 format). No kernel here reads a table — each walks the filter taps with offsets
+// held in registers — so the builders serve kernels registered with needs_lut (ExecutionPlan uploads the table).
+#include <cstdint>
+#include <limits>
 #include <set>
 #include <sstream>
 
@@ -66,6 +69,42 @@ std::vector<const KernelDesc*> kernels_for_backend(Backend b) {
   for (const auto& k : kernel_registry())
     if (b == Backend::kAuto || k.backend == b) out.push_back(&k);
   return out;
+}
+
+namespace {
+// Offsets are 32-bit element counts: the channel displacement (C - 1) * H * W and the dilated tap extents must fit.
+void check_table_range(const Conv2DParams& p) {
+  const int64_t plane = int64_t(p.in_h) * p.in_w;
+  const int64_t lim = std::numeric_limits<int32_t>::max();
+  GIE_REQUIRE(p.in_channels > 0 && p.kernel_h > 0 && p.kernel_w > 0 && plane > 0, StatusCode::kInvalidArgument,
+              "gather table of an empty problem");
+  GIE_REQUIRE(int64_t(p.in_channels) * plane <= lim &&
+                  int64_t(p.kernel_h) * p.dilation_h <= lim && int64_t(p.kernel_w) * p.dilation_w <= lim,
+              StatusCode::kUnsupported, "gather-table offsets exceed 32 bits");
+}
+}  // namespace
+
+std::vector<LutEntry> build_conv_lut(const Conv2DParams& p) {
+  check_table_range(p);
+  const int32_t plane = p.in_h * p.in_w;
+  std::vector<LutEntry> table;
+  table.reserve(size_t(p.gemm_k()));
+  for (int c = 0; c < p.in_channels; ++c)  // k = (c * KH + r) * KW + s
+    for (int r = 0; r < p.kernel_h; ++r)
+      for (int s = 0; s < p.kernel_w; ++s) table.push_back({c * plane, r * p.dilation_h, s * p.dilation_w, 0});
+  return table;
+}
+
+std::vector<LutEntry> build_conv_lut_chunked(const Conv2DParams& p) {
+  check_table_range(p);
+  GIE_REQUIRE(p.in_channels % 8 == 0, StatusCode::kInvalidArgument,
+              "chunked gather table needs in_channels % 8 == 0 (in_channels = " + std::to_string(p.in_channels) + ")");
+  std::vector<LutEntry> table;
+  table.reserve(size_t(p.gemm_k() / 8));
+  for (int r = 0; r < p.kernel_h; ++r)  // q = (r * KW + s) * C/8 + chunk: taps outer, 8-channel chunks inner
+    for (int s = 0; s < p.kernel_w; ++s)
+      for (int c8 = 0; c8 < p.in_channels; c8 += 8) table.push_back({c8, r * p.dilation_h, s * p.dilation_w, 0});
+  return table;
 }
 
 }  // namespace gie

@@ -117,6 +117,8 @@ _CAPI = {
     "gie_plan_destroy": ([_vp], _i),
     "gie_plan_workspace_bytes": ([_vp, ctypes.POINTER(_sz)], _i),
     "gie_plan_kernel_name": ([_vp, _cp, _sz], _i),
+    "gie_plan_lut_bytes": ([_vp, ctypes.POINTER(_sz)], _i),
+    "gie_build_conv_lut": ([_PP, _i, ctypes.POINTER(ctypes.c_int32), ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)], _i),
     "gie_plan_execute": ([_vp, _TP, _TP, _TP, _TP, _vp, _sz, _vp], _i),
     "gie_plan_execute_unchecked": ([_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i),
     "gie_plan_time": ([_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _i, _i, ctypes.c_double, _dp, _ip], _i),
@@ -145,6 +147,7 @@ _CAPI = {
     "gie_device_cu_count": ([_i, _ip], _i),
     "gie_build_fingerprint": ([_cp, _sz], _i),
     "gie_testing_add_faulty_kernels": ([_i], _i),
+    "gie_testing_add_lut_probe_kernels": ([], _i),
     "gie_graph_create": ([ctypes.POINTER(_vp)], _i),
     "gie_graph_destroy": ([_vp], _i),
     "gie_graph_capture_chain": ([_vp, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
@@ -599,6 +602,12 @@ class Plan:
     def kernel(self) -> str:
         return _str_out(capi().gie_plan_kernel_name, self.h)
 
+    @property
+    def lut_bytes(self) -> int:
+        n = ctypes.c_size_t()
+        check(capi().gie_plan_lut_bytes(self.h, ctypes.byref(n)))
+        return n.value
+
     def execute(self, t: ConvTensors, ws: DeviceBuffer | None, stream: Stream | None = None, **override):
         x, w, b, y = t.tensors()
         pass_bias = override.pop("bias", True)
@@ -631,6 +640,18 @@ class Plan:
                                           ws.addr if ws else None, ws.nbytes if ws else 0, stream.h, iters, us),
               "stage timing")
         return {"repack_us": us[0], "gemm_us": us[1], "reduce_us": us[2]}
+
+
+def build_conv_lut(p: Problem, chunked: bool = False) -> np.ndarray:
+    """build_conv_lut / build_conv_lut_chunked (kernel_registry.h:86-96) -> int32[entries, 4]"""
+    pc = p.c()
+    n = ctypes.c_int64()
+    check(capi().gie_build_conv_lut(ctypes.byref(pc), int(chunked), None, 0, ctypes.byref(n)), "build_conv_lut")
+    out = np.empty((n.value, 4), np.int32)
+    check(capi().gie_build_conv_lut(ctypes.byref(pc), int(chunked),
+                                    out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), n.value, ctypes.byref(n)),
+          "build_conv_lut")
+    return out
 
 
 def registry() -> list[str]:

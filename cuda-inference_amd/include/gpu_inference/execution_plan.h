@@ -31,7 +31,8 @@ class ExecutionPlan {
   const ConvProblem& problem() const { return problem_; }
   const KernelDesc& kernel() const { return *kernel_; }
   size_t workspace_bytes() const { return workspace_bytes_; }
-  size_t persistent_bytes() const { return persistent_bytes_; }
+  size_t persistent_bytes() const { return persistent_bytes_ + lut_bytes_; }  // plan-owned, the gather table included
+  size_t lut_bytes() const { return lut_bytes_; }                             // 0 unless the kernel sets needs_lut
   int device() const { return device_; }
 
  private:
@@ -41,6 +42,8 @@ class ExecutionPlan {
   int device_ = 0;
   size_t workspace_bytes_ = 0;
   size_t persistent_bytes_ = 0;
+  DeviceBuffer lut_;  // device copy of the gather table (needs_lut kernels)
+  size_t lut_bytes_ = 0;
   size_t x_bytes_ = 0, w_bytes_ = 0, y_bytes_ = 0, bias_bytes_ = 0;  // operand footprints, for the alias checks
   LaunchArgs proto_;  // everything but the pointers and the stream, filled once by create()
   std::shared_ptr<void> state_;

@@ -31,6 +31,7 @@ struct LaunchArgs {
   void* y = nullptr;
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
+  const void* plan_data = nullptr;  // device copy of the plan's gather table when the kernel sets needs_lut
   void* plan_state = nullptr;       // opaque per-plan state created by KernelDesc::create_state
   hipStream_t stream = nullptr;
   // Profiling hook: >= 0 launches only that stage of a multi-launch kernel (0 = repack, 1 = main kernel,
@@ -49,6 +50,8 @@ struct KernelDesc {
   // Tile extents in the implicit-GEMM view (M = C_out, N = B*Ho*Wo, K = C_in*Kh*Kw).
   int tile_m = 1, tile_n = 1, tile_k = 1;
   bool uses_tensor_cores = false;  // matrix cores (MFMA)
+  bool needs_lut = false;    // the plan builds the gather table (build_conv_lut*) and passes it as plan_data
+  bool lut_chunked = false;  // ... one entry per 8 consecutive k (build_conv_lut_chunked, C % 8 == 0)
   int launches = 1;             // kernel launches per forward call (cost model)
   double efficiency_prior = 0;  // compute-ceiling fraction for a family the cost model has no measured profile of
   double (*extra_traffic_bytes)(const ConvProblem&) = nullptr;  // DRAM bytes beyond compulsory X/W/Y
@@ -73,5 +76,21 @@ const std::vector<KernelDesc>& kernel_registry();
 std::vector<KernelDesc>& kernel_registry_for_testing();
 const KernelDesc* find_kernel(const std::string& name);
 std::vector<const KernelDesc*> kernels_for_backend(Backend b);
+
+// Gather table for implicit-GEMM kernels that walk the reduction index k in (c, r, s) order (the reference's
+// kernel_registry.h:86-96 format, 16 bytes per entry). No kernel of this library reads one — every family here
+// keeps its tap offsets in registers — but a kernel registered with needs_lut gets it built and uploaded once per
+// plan, as in the reference.
+struct alignas(16) LutEntry {
+  int32_t c_off;  // channel displacement: c * H * W elements (per k), 8 * chunk elements (chunked)
+  int32_t r_off;  // filter-row displacement r * dilation_h
+  int32_t s_off;  // filter-column displacement s * dilation_w
+  int32_t pad_;   // zero
+};
+// One entry per k = (c * KH + r) * KW + s, k < C * KH * KW.
+std::vector<LutEntry> build_conv_lut(const Conv2DParams& p);
+// One entry per chunk q of 8 consecutive k in tap-major order (q = (r * KW + s) * C/8 + c/8); C % 8 == 0 or it
+// throws kInvalidArgument.
+std::vector<LutEntry> build_conv_lut_chunked(const Conv2DParams& p);
 
 }  // namespace gie

@@ -68,6 +68,11 @@ int gie_plan_create(const gie_problem* p, const char* kernel_name, int device, v
 int gie_plan_destroy(void* plan);
 int gie_plan_workspace_bytes(void* plan, size_t* bytes);
 int gie_plan_kernel_name(void* plan, char* buf, size_t n);
+/* bytes of the plan's device gather table (execution_plan.cpp:69-73; 0 unless the kernel sets needs_lut) */
+int gie_plan_lut_bytes(void* plan, size_t* bytes);
+/* build_conv_lut / build_conv_lut_chunked (kernel_registry.h:86-96, conv_common.cu:22-50): *count entries of four
+   int32 (c_off, r_off, s_off, 0); out4 == NULL asks for the count only, cap is out4's capacity in entries */
+int gie_build_conv_lut(const gie_problem* p, int chunked, int32_t* out4, int64_t cap, int64_t* count);
 int gie_plan_execute(void* plan, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
                      const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream);
 int gie_plan_execute_unchecked(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
@@ -149,6 +154,10 @@ int gie_build_fingerprint(char* buf, size_t n);
    kernel to the registry so tests can prove the autotuner never selects it. kind 0: fast but wrong (fills y with
    a constant), kind 1: its launch throws. Names: "test_garbage_<p>" / "test_throwing_<p>" per precision. */
 int gie_testing_add_faulty_kernels(int kind);
+/* TESTING ONLY: appends needs_lut probe kernels "test_lut_probe_<p>" and "test_lut_chunked_probe_<p>" that run only
+   2x3 filters over 24 input channels and copy the plan's device gather table into y, so a test can read back what
+   ExecutionPlan::create uploaded (execution_plan.cpp:69-73, :133). */
+int gie_testing_add_lut_probe_kernels(void);
 
 /* ---- HipGraphExecutor (cuda_graph.h:14-46) over a chain of plan executions ---- */
 int gie_graph_create(void** graph);

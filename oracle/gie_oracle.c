@@ -311,6 +311,21 @@ void gie_oracle_repack_c_hw(const uint16_t* src, uint16_t* dst, int batch, int C
   }
 }
 
+/* conv_common.cu:22-37: one entry per k, k = c * KH * KW + r * KW + s (the unchunked gather table) */
+int64_t gie_oracle_lut(const gie_oracle_params* p, int32_t* out4) {
+  const int khw = p->kernel_h * p->kernel_w;
+  const int64_t n = (int64_t)p->in_channels * khw;
+  if (out4 == NULL) return n;
+  for (int64_t k = 0; k < n; ++k) {
+    const int c = (int)(k / khw), rs = (int)(k % khw);
+    out4[4 * k + 0] = (int32_t)((int64_t)c * p->in_h * p->in_w);
+    out4[4 * k + 1] = (rs / p->kernel_w) * p->dilation_h;
+    out4[4 * k + 2] = (rs % p->kernel_w) * p->dilation_w;
+    out4[4 * k + 3] = 0;
+  }
+  return n;
+}
+
 /* conv_common.cu:39-50 with the channel count generalised to the padded count C_pad = in_channels here */
 int64_t gie_oracle_lut_chunked(const gie_oracle_params* p, int32_t* out4) {
   if (p->in_channels % 8 != 0) return -1;

@@ -13,6 +13,7 @@
  *   Rng (SplitMix64)      src/runtime/testing.cu:12-24
  *   make_conv_data        src/runtime/testing.cu:63-105 (draw order x, w, bias)
  *   transpose_c_hw        src/kernels/tensor_core_mma.cu:61-82,309-310 (activation / weight repack)
+ *   build_conv_lut       src/kernels/conv_common.cu:22-37
  *   build_conv_lut_chunked src/kernels/conv_common.cu:39-50
  *   split-K partition     src/kernels/tensor_core_mma.cu:112-115
  *   splitk_reduce         src/kernels/tensor_core_mma.cu:254-262
@@ -85,6 +86,9 @@ void gie_oracle_compare(const float* test, const float* ref, const float* scale,
 
 /* 16-bit permutation dst[b][hw][c] = src[b][c][hw]; channels c in [C, C_pad) are zero in dst. */
 void gie_oracle_repack_c_hw(const uint16_t* src, uint16_t* dst, int batch, int C, int HW, int C_pad);
+
+/* one entry per k (c-major): {c * H * W, r * dilation_h, s * dilation_w, 0}; out4 NULL: the count only */
+int64_t gie_oracle_lut(const gie_oracle_params* p, int32_t* out4);
 
 /* one entry per 8 consecutive k for (r,s,c) ordering: {c_off, r_off, s_off, 0} */
 int64_t gie_oracle_lut_chunked(const gie_oracle_params* p, int32_t* out4);

@@ -94,6 +94,8 @@ def lib():
         L.gie_oracle_repack_c_hw.argtypes = [u16p, u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.gie_oracle_lut_chunked.argtypes = [P, ctypes.POINTER(ctypes.c_int32)]
         L.gie_oracle_lut_chunked.restype = ctypes.c_int64
+        L.gie_oracle_lut.argtypes = [P, ctypes.POINTER(ctypes.c_int32)]
+        L.gie_oracle_lut.restype = ctypes.c_int64
         L.gie_oracle_splitk_range.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                               ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
         L.gie_oracle_splitk_reduce.argtypes = [fp, fp, fp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -268,6 +270,15 @@ def repack_c_hw(src_bits: np.ndarray, batch: int, C: int, HW: int, C_pad: int | 
     dst = np.empty(batch * HW * C_pad, np.uint16)
     lib().gie_oracle_repack_c_hw(_u16(src), _u16(dst), batch, C, HW, C_pad)
     return dst
+
+
+def lut(c: Conv) -> np.ndarray:
+    """conv_common.cu:22-37 -> int32[C*KH*KW, 4]"""
+    p = c.params()
+    n = lib().gie_oracle_lut(ctypes.byref(p), None)
+    out = np.empty((n, 4), np.int32)
+    lib().gie_oracle_lut(ctypes.byref(p), out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)))
+    return out
 
 
 def lut_chunked(c: Conv) -> np.ndarray:

@@ -246,3 +246,20 @@ def test_stack_configuration_table_and_geometry_on_host():
               gie.Problem(1, 64, 40, 7, 32, 3, 3, 1, 1, 1, 1, precision="fp16")):  # images taller than every stack
         for i in range(n):
             assert h.gie_hip_stack_check(i, ctypes.byref(p.geom(p.in_channels)), None, None) != 0
+
+
+@pytest.mark.parametrize("shape", [(1, 24, 9, 9, 4, 3, 3, 1, 1, 1, 1, 1), (2, 16, 7, 5, 8, 2, 3, 1, 1, 0, 0, 2),
+                                   (1, 64, 14, 14, 32, 1, 1, 1, 1, 0, 0, 1), (1, 8, 30, 30, 4, 7, 7, 2, 2, 3, 3, 1)])
+def test_gather_table_builders_match_oracle(shape):
+    """build_conv_lut / build_conv_lut_chunked (kernel_registry.h:86-96) against the oracle's restatement of
+    conv_common.cu:22-50, bit for bit, with and without dilation; the chunked form rejects C % 8 != 0."""
+    B, C, H, W, Oc, Kh, Kw, Sh, Sw, Ph, Pw, dil = shape
+    p = gie.Problem(B, C, H, W, Oc, Kh, Kw, Sh, Sw, Ph, Pw, precision="fp16", has_bias=False, relu=False)
+    p.dilation_h = p.dilation_w = dil
+    c = O.P(B, C, H, W, Oc, Kh, Kw, Sh, Sw, Ph, Pw, dilation_h=dil, dilation_w=dil)
+    assert np.array_equal(gie.build_conv_lut(p), O.lut(c))
+    assert np.array_equal(gie.build_conv_lut(p, chunked=True), O.lut_chunked(c))
+    odd = gie.Problem(1, 12, 5, 5, 4, 3, 3, 1, 1, 1, 1, precision="fp16", has_bias=False, relu=False)
+    with pytest.raises(gie.GieError):
+        gie.build_conv_lut(odd, chunked=True)
+    assert gie.build_conv_lut(odd).shape == (12 * 9, 4)

@@ -243,6 +243,30 @@ def test_incorrect_or_failing_candidates_are_never_selected(tmp_path):
     assert r["best_us"] > 0
 
 
+@pytest.mark.parametrize("precision", ["fp16", "bf16"])
+@pytest.mark.parametrize("chunked", [False, True])
+def test_plan_uploads_the_gather_table_of_a_needs_lut_kernel(precision, chunked):
+    """execution_plan.cpp:69-73,133: a kernel registered with needs_lut gets its gather table built once per plan,
+    uploaded to the device and passed as plan_data. The probe kernel copies plan_data into y; the bytes must be the
+    oracle's table (conv_common.cu:22-50). Kernels without needs_lut own no table."""
+    gie.check(gie.capi().gie_testing_add_lut_probe_kernels())
+    p = P(1, 24, 9, 8, 64, 2, 3, 1, 1, 0, 0, precision=precision, bias=False, relu=False)
+    name = ("test_lut_chunked_probe_" if chunked else "test_lut_probe_") + precision
+    plan = gie.Plan(p, name)
+    c = O.P(1, 24, 9, 8, 64, 2, 3, 1, 1, 0, 0)
+    want = O.lut_chunked(c) if chunked else O.lut(c)
+    assert plan.lut_bytes == want.nbytes
+    y = gie.DeviceBuffer(int(np.prod(p.y_shape())) * 2)
+    assert y.nbytes >= want.nbytes
+    y.fill(0xFF)
+    plan.execute_raw(0, 0, None, y.addr, None, 0)
+    gie.synchronize()
+    got = y.download(np.int32, want.size).reshape(want.shape)
+    assert np.array_equal(got, want)
+    assert gie.Plan(P(1, 24, 9, 8, 64, 3, 3, 1, 1, 1, 1, precision=precision), K16 if precision == "fp16"
+                    else K16.replace("fp16", "bf16")).lut_bytes == 0
+
+
 def test_search_space_and_cost_are_reported(tmp_path):
     p = P(2, 32, 14, 14, 32, 3, 3, 1, 1, 1, 1)
     r = gie.autotune(p, cache_path=_cache(tmp_path, "space"), samples=5, warmup=2, min_sample_ms=0.2)

@@ -293,6 +293,32 @@ def test_lut_chunked_closed_form():
         O.lut_chunked(P(1, 3, 9, 9, 4, 3, 3, 1, 1, 1, 1))
 
 
+@pytest.mark.parametrize("dil", [1, 2])
+def test_lut_gather_reproduces_the_convolution(dil):
+    """The per-k table, used as an implicit-GEMM gather (column k of the patch matrix for output (oh, ow) is
+    x[c_off + (oh + r_off) * W + ow + s_off]) against weights flattened in OIHW order, gives the convolution
+    computed window by window; dilation 1 also against the oracle's own convolution."""
+    c = P(1, 5, 9, 11, 3, 3, 2, 1, 1, 0, 0, dilation_h=dil, dilation_w=dil)
+    t = O.lut(c)
+    assert t.shape == (c.gemm_k, 4) and np.all(t[:, 3] == 0)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((c.in_channels, c.in_h, c.in_w))
+    w = rng.standard_normal((c.out_channels, c.in_channels, c.kernel_h, c.kernel_w))
+    oh, ow = c.in_h - dil * (c.kernel_h - 1), c.in_w - dil * (c.kernel_w - 1)
+    gy, gx = np.meshgrid(np.arange(oh), np.arange(ow), indexing="ij")
+    cols = np.stack([x.ravel()[e[0] + (gy + e[1]) * c.in_w + gx + e[2]] for e in t])  # [K, oh, ow]
+    y_lut = w.reshape(c.out_channels, -1) @ cols.reshape(c.gemm_k, -1)
+    y_win = np.zeros((c.out_channels, oh, ow))
+    for ci in range(c.in_channels):
+        for r in range(c.kernel_h):
+            for s in range(c.kernel_w):
+                y_win += w[:, ci, r, s, None, None] * x[ci, r * dil:r * dil + oh, s * dil:s * dil + ow]
+    assert np.allclose(y_lut.reshape(y_win.shape), y_win, rtol=1e-12, atol=1e-12)
+    if dil == 1:
+        y_ref, _ = O.conv2d(prob(c), x.ravel(), w.ravel(), None)
+        assert np.allclose(y_lut.ravel(), y_ref.ravel(), rtol=1e-5, atol=1e-5)  # the oracle reads float32 x, w
+
+
 @pytest.mark.parametrize("ktiles,split", [(144, 1), (144, 2), (144, 8), (9, 4), (10, 3), (7, 8)])
 def test_splitk_ranges_partition_the_k_tiles(ktiles, split):
     rs = [O.splitk_range(ktiles, z, split) for z in range(split)]
