@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256 * KH, 1) void stack_kernel(const uint16_t* __re
                                                       float* __restrict__ partial, StackGeom g) {
   using Sh = StackShape<P, NBW, KH>;
   using Sc = StackSched<P, NBW>;
-  constexpr int CS = Sh::CS, NW = Sh::NW, NT = Sh::NT, RW = Sh::RW, NR = Sh::NR, NBR = Sh::NBR;
+  constexpr int CS = Sh::CS, NW = Sh::NW, NT = Sh::NT, RW = Sh::RW, NBR = Sh::NBR;
   constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
   constexpr int ACT = Sh::ACT, KR = Sh::KR;
   constexpr int WOFF = 2 * ACT;  // LDS: [2 activation stages][2 weight stages]
@@ -492,7 +492,7 @@ StackShapeInfo stack_shape_of() {
 template <int... Is>
 StackShapeInfo stack_info(int cfg, std::integer_sequence<int, Is...>) {
   StackShapeInfo si{};
-  ((cfg == Is ? (si = stack_shape_of<Is>(), true) : false), ...);
+  ((cfg == Is ? void(si = stack_shape_of<Is>()) : void()), ...);
   return si;
 }
 

@@ -86,7 +86,8 @@ void HipGraphExecutor::capture(const Enqueue& enqueue) {
     GIE_HIP_CHECK(hipStreamSynchronize(warm.get()));
   }
   double us = 0;
-  adopt(record(enqueue, &us), us);
+  hipGraph_t g = record(enqueue, &us);  // recorded before `us` is read (argument order is unspecified)
+  adopt(g, us);
 }
 
 bool HipGraphExecutor::recapture_update(const Enqueue& enqueue) {

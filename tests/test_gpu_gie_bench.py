@@ -88,3 +88,31 @@ def test_gie_bench_rows_on_gpu(tmp_path):
     assert r["stage_repack_us"] > 0 and r["stage_conv_us"] > 0 and "stage_reduce_us" not in r
     meta = json.load(open(out / "meta.json"))
     assert "gfx950" in meta["arch"] and meta["cu_count"] > 0
+
+
+GRAPH_BIN = os.path.join(ROOT, "cuda-inference_amd", "lib", "gie_graph_bench")
+
+
+@pytest.mark.parametrize("precision", ["fp16", "bf16"])
+def test_graph_bench_chain_records(tmp_path, precision):
+    """gie_graph_bench (the reference's benchmarks/graph_bench.cpp measurements): for the first chain case at two
+    depths, the graph replays reproduce the eager chain bit for bit, the graph holds one node per layer launch, and
+    every timing is positive; the stream-concurrency rows cover 2, 4 and 8 independent convolutions."""
+    cmd = [GRAPH_BIN, "--out", str(tmp_path), "--precision", precision, "--cases", "1", "--depths", "1,4"]
+    print(" ".join(cmd), flush=True)
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    print(p.stdout[-2000:], p.stderr[-2000:], flush=True)
+    assert p.returncode == 0, p.stderr[-2000:]
+    rows = [json.loads(line) for line in open(tmp_path / "graphs.jsonl")]
+    chains = [r for r in rows if r["experiment"] == "F_hip_graphs"]
+    assert [r["layers"] for r in chains] == [1, 4]
+    for r in chains:
+        assert r["case"] == "b1_c32_14x14_k3" and r["precision"] == precision
+        assert r["bitwise_identical_replays"] is True
+        assert r["graph_nodes"] >= r["layers"]
+        for k in ("capture_us", "instantiate_us", "eager_device_us", "graph_device_us", "eager_host_launch_us",
+                  "graph_host_launch_us"):
+            assert r[k] > 0, (k, r)
+    conc = [r for r in rows if r["experiment"] == "F_stream_concurrency"]
+    assert [r["independent_convs"] for r in conc] == [2, 4, 8]
+    assert all(r["one_stream_us"] > 0 and r["multi_stream_us"] > 0 for r in conc)
