@@ -287,7 +287,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the Conv2D library is a "
-              "single-GPU operator; see DESIGN.md for how it would shard by batch).", file=sys.stderr)
+              "single-GPU operator; across GPUs each rank would run its own share of the batch with the same "
+              "weights, no collective in the forward pass).", file=sys.stderr)
         sys.exit(2)
 
     import gie
