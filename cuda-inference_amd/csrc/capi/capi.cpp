@@ -301,6 +301,16 @@ int gie_plan_workspace_bytes(void* plan, size_t* bytes) {
   return guarded([&] { *bytes = plan_of(plan).workspace_bytes(); });
 }
 
+int gie_plan_execute_staged(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                            size_t workspace_bytes, void* stream, void* const* events3) {
+  return guarded([&] {
+    GIE_REQUIRE(events3 != nullptr, StatusCode::kInvalidArgument, "null stage events");
+    hipEvent_t ev[3] = {static_cast<hipEvent_t>(events3[0]), static_cast<hipEvent_t>(events3[1]),
+                        static_cast<hipEvent_t>(events3[2])};
+    plan_of(plan).execute_unchecked(x, w, bias, y, workspace, workspace_bytes, static_cast<hipStream_t>(stream), ev);
+  });
+}
+
 int gie_plan_lut_bytes(void* plan, size_t* bytes) {
   return guarded([&] { *bytes = plan_of(plan).lut_bytes(); });
 }
@@ -382,9 +392,9 @@ int gie_plan_time_stages(void* plan, const void* x, const void* w, const void* b
     GIE_HIP_CHECK(hipEventCreate(&e1));
     pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s);
     for (int k = 0; k < 3; ++k) {
-      pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, k);  // warm this stage
+      pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, nullptr, k);  // warm this stage
       GIE_HIP_CHECK(hipEventRecord(e0, s));
-      for (int it = 0; it < iters; ++it) pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, k);
+      for (int it = 0; it < iters; ++it) pl.execute_unchecked(x, w, bias, y, workspace, workspace_bytes, s, nullptr, k);
       GIE_HIP_CHECK(hipEventRecord(e1, s));
       GIE_HIP_CHECK(hipEventSynchronize(e1));
       float ms = 0;

@@ -156,14 +156,17 @@ struct Fns {
     float* part = en.split > 1 ? reinterpret_cast<float*>(ws + l.part_off) : nullptr;
     void* s = la.stream;
     const auto stage = [&](int k) { return la.only_stage < 0 || la.only_stage == k; };
+    record_stage_event(la, 0);
     if (stage(0)) {
       check_kernel_status(gie_hip_repack_w_blocked(la.w, wk, &g, s), "channel-blocked weight repack");
     }
+    record_stage_event(la, 1);
     if (stage(1)) {
       check_kernel_status(gie_hip_conv_band(en.config, dtype_of(prob.precision), &g, la.x, wk, la.bias, la.y, part,
                                           en.split, s),
                         "band MFMA convolution (direct NCHW)");
     }
+    record_stage_event(la, 2);
     if (en.split > 1 && stage(2)) {
       check_kernel_status(gie_hip_splitk_reduce(dtype_of(prob.precision), part, la.bias, la.y,
                                                 prob.p.output_shape().numel(), en.split, prob.p.out_channels,

@@ -108,7 +108,7 @@ ExecutionPlan::~ExecutionPlan() = default;
 
 void ExecutionPlan::execute(const ConstTensorRef& x, const ConstTensorRef& w, const ConstTensorRef* bias,
                             const TensorRef& y, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                            int only_stage) const {
+                            hipEvent_t* stage_events, int only_stage) const {
   const Conv2DParams& p = problem_.p;
   const DataType dt = problem_.dtype();
   expect_operand("input x", x.data, x.dtype, x.shape, dt, p.input_shape());
@@ -145,11 +145,12 @@ void ExecutionPlan::execute(const ConstTensorRef& x, const ConstTensorRef& w, co
   if (current != device_)
     bad_argument("plan belongs to device " + std::to_string(device_) + " but device " + std::to_string(current) +
                  " is current");
-  execute_unchecked(x.data, w.data, b, y.data, workspace, workspace_bytes, stream, only_stage);
+  execute_unchecked(x.data, w.data, b, y.data, workspace, workspace_bytes, stream, stage_events, only_stage);
 }
 
 void ExecutionPlan::execute_unchecked(const void* x, const void* w, const void* bias, void* y, void* workspace,
-                                      size_t workspace_bytes, hipStream_t stream, int only_stage) const {
+                                      size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events,
+                                      int only_stage) const {
   RoctxRange range(kernel_->name.c_str());
   LaunchArgs la = proto_;
   la.x = x;
@@ -159,6 +160,7 @@ void ExecutionPlan::execute_unchecked(const void* x, const void* w, const void* 
   la.workspace = workspace;
   la.workspace_bytes = workspace_bytes;
   la.stream = stream;
+  la.stage_events = stage_events;
   la.only_stage = only_stage;
   kernel_->launch(la);
 }

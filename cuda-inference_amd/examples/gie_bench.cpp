@@ -462,7 +462,7 @@ void measure(Bench& b, const ConvProblem& prob, Inputs& in, const KernelDesc& k,
   void* y = in.dev.dy.data();
   auto run = [&](hipStream_t s, int only_stage) {
     plan->execute_unchecked(in.dev.dx.data(), in.dev.dw.data(), unfused ? nullptr : bias, y, ws.data(), ws.size(), s,
-                            only_stage);
+                            nullptr, only_stage);
     if (unfused && only_stage < 0) {
       if (prob.has_bias) launch_bias_add(prob.p, prob.precision, bias, y, s);
       if (prob.activation == Activation::kReLU) launch_relu(prob.p, prob.precision, y, s);

@@ -118,6 +118,7 @@ _CAPI = {
     "gie_plan_workspace_bytes": ([_vp, ctypes.POINTER(_sz)], _i),
     "gie_plan_kernel_name": ([_vp, _cp, _sz], _i),
     "gie_plan_lut_bytes": ([_vp, ctypes.POINTER(_sz)], _i),
+    "gie_plan_execute_staged": ([_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_vp)], _i),
     "gie_build_conv_lut": ([_PP, _i, ctypes.POINTER(ctypes.c_int32), ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)], _i),
     "gie_plan_execute": ([_vp, _TP, _TP, _TP, _TP, _vp, _sz, _vp], _i),
     "gie_plan_execute_unchecked": ([_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i),

@@ -21,12 +21,15 @@ class ExecutionPlan {
 
   // Validates arguments (shapes, dtypes, null pointers, aliasing, workspace size) and launches asynchronously
   // on `stream`. Never synchronizes the device.
+  // stage_events: optional, three events recorded around the repack and convolution stages (LaunchArgs).
   void execute(const ConstTensorRef& x, const ConstTensorRef& w, const ConstTensorRef* bias, const TensorRef& y,
-               void* workspace, size_t workspace_bytes, hipStream_t stream, int only_stage = -1) const;
+               void* workspace, size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events = nullptr,
+               int only_stage = -1) const;
 
   // Raw-pointer fast path: arguments were validated once by the caller (timing loops, graph capture).
   void execute_unchecked(const void* x, const void* w, const void* bias, void* y, void* workspace,
-                         size_t workspace_bytes, hipStream_t stream, int only_stage = -1) const;
+                         size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events = nullptr,
+                         int only_stage = -1) const;
 
   const ConvProblem& problem() const { return problem_; }
   const KernelDesc& kernel() const { return *kernel_; }

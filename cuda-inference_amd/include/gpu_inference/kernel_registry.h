@@ -34,6 +34,9 @@ struct LaunchArgs {
   const void* plan_data = nullptr;  // device copy of the plan's gather table when the kernel sets needs_lut
   void* plan_state = nullptr;       // opaque per-plan state created by KernelDesc::create_state
   hipStream_t stream = nullptr;
+  // Optional stage events (the reference's hook): families with a repack stage record events[0] before it,
+  // events[1] after it and events[2] after the convolution (before any split-K reduce).
+  hipEvent_t* stage_events = nullptr;
   // Profiling hook: >= 0 launches only that stage of a multi-launch kernel (0 = repack, 1 = main kernel,
   // 2 = split-K reduce) on a workspace a full launch has already filled; every stage is idempotent, so
   // back-to-back launches of one stage time that kernel alone. -1 (default) launches the whole chain.
@@ -70,6 +73,11 @@ struct KernelDesc {
 
   std::string describe() const;
 };
+
+// Records stage event i of a full launch when the caller passed stage events (LaunchArgs::stage_events).
+inline void record_stage_event(const LaunchArgs& la, int i) {
+  if (la.stage_events != nullptr && la.only_stage < 0) GIE_HIP_CHECK(hipEventRecord(la.stage_events[i], la.stream));
+}
 
 const std::vector<KernelDesc>& kernel_registry();
 // TESTING ONLY: mutable access so tests can inject deliberately faulty kernels.

@@ -68,6 +68,10 @@ int gie_plan_create(const gie_problem* p, const char* kernel_name, int device, v
 int gie_plan_destroy(void* plan);
 int gie_plan_workspace_bytes(void* plan, size_t* bytes);
 int gie_plan_kernel_name(void* plan, char* buf, size_t n);
+/* execute_unchecked with stage events (execution_plan.cpp:122-136, im2col.cu:88-114): a family with a repack stage
+   records events3[0] before it, events3[1] after it and events3[2] after the convolution; others record none */
+int gie_plan_execute_staged(void* plan, const void* x, const void* w, const void* bias, void* y, void* workspace,
+                            size_t workspace_bytes, void* stream, void* const* events3);
 /* bytes of the plan's device gather table (execution_plan.cpp:69-73; 0 unless the kernel sets needs_lut) */
 int gie_plan_lut_bytes(void* plan, size_t* bytes);
 /* build_conv_lut / build_conv_lut_chunked (kernel_registry.h:86-96, conv_common.cu:22-50): *count entries of four

@@ -2,6 +2,7 @@
 tests/test_validation.cpp, test_dispatcher.cpp, test_autotuner.cu, test_cuda_graph.cu and
 test_runtime_concurrency.cu with this library's MFMA kernel names. Every call goes through the C-ABI
 (include/gie_capi.h) into the gie:: C++ runtime."""
+import ctypes
 import json
 import os
 import threading
@@ -265,6 +266,28 @@ def test_plan_uploads_the_gather_table_of_a_needs_lut_kernel(precision, chunked)
     assert np.array_equal(got, want)
     assert gie.Plan(P(1, 24, 9, 8, 64, 3, 3, 1, 1, 1, 1, precision=precision), K16 if precision == "fp16"
                     else K16.replace("fp16", "bf16")).lut_bytes == 0
+
+
+@pytest.mark.parametrize("kernel", [K16, "mfma_fp16_64x64x32_w2x2_s4_sk4"])
+def test_stage_events_bracket_repack_and_convolution(kernel):
+    """execution_plan.cpp:122-136 / im2col.cu:88-114: stage events passed to execute are recorded before the
+    repack, after it and after the convolution (before any split-K reduce), on the caller's stream, and the call's
+    result is unchanged."""
+    p = P(2, 64, 12, 12, 24, 3, 3, 1, 1, 1, 1)  # K = 576: long enough for split 4
+    b = Bundle(p, 5)
+    plan = gie.Plan(p, kernel)
+    ws = gie.DeviceBuffer(plan.workspace_bytes) if plan.workspace_bytes else None
+    st = gie.Stream()
+    ev = [gie.Event() for _ in range(3)]
+    evs = (ctypes.c_void_p * 3)(*[e.h.value for e in ev])
+    b.t.poison()
+    gie.check(gie.capi().gie_plan_execute_staged(plan.h, b.t.dx.addr, b.t.dw.addr, b.t.bias_addr(), b.t.dy.addr,
+                                                   ws.addr if ws else None, ws.nbytes if ws else 0, st.h, evs),
+              "execute with stage events")
+    st.sync()
+    repack_ms, conv_ms = ev[0].elapsed_ms(ev[1]), ev[1].elapsed_ms(ev[2])
+    assert repack_ms > 0 and conv_ms > 0, (repack_ms, conv_ms)
+    assert b.compare(b.t.y()).passed()
 
 
 def test_search_space_and_cost_are_reported(tmp_path):
