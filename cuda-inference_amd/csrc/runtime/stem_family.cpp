@@ -97,7 +97,7 @@ KernelDesc make_entry() {
   KernelDesc k;
   k.name = std::string("stem_") + to_string(P) + "_7x7s2_64x32x16_wreg";
   k.backend = Backend::kTensorCore;
-  k.version = 1;
+  k.version = 2;  // 2: device-scope output stores
   k.params = {{"block_m", 64}, {"block_n", 32}, {"block_k", 16}, {"kernel_h", 7}, {"kernel_w", 7},
               {"stages", 1},   {"split_k", 1}};
   k.threads_per_block = 512;
