@@ -3,7 +3,8 @@
 // deterministic run to run. HBM-bound: reads split*4 B and writes 2 B per output. Each thread owns 4
 // consecutive outputs: 16-byte partial loads (when every slice start is 16-byte aligned) and one 8-byte store
 // when the destination allows it; a grid-stride loop keeps the grid bounded. Index arithmetic is 32-bit with
-// magic-number divisions below 2^30 outputs (64-bit divisions per output cost more than the loads).
+// magic-number divisions when every partial offset z * total + i fits an int (64-bit divisions per output cost
+// more than the loads); otherwise 64-bit throughout.
 #include "device_common.h"
 
 namespace gie_hip {
@@ -18,8 +19,8 @@ struct Div30 {
 };
 __device__ __forceinline__ int div30(int n, Div30 d) { return int((__umulhi(unsigned(n), d.mg) + unsigned(n)) >> d.sh); }
 
-// Outputs below 2^30 (every case the conv kernels produce): 32-bit indices, the channel of a quad's first output by
-// two magic-number divisions and the later ones by counting the plane crossings (hw_out may be below 4). NS > 0: the
+// Partial offsets below 2^31 (split * total): 32-bit indices, the channel of a quad's first output by two
+// magic-number divisions and the later ones by counting the plane crossings (hw_out may be below 4). NS > 0: the
 // split factor is a compile-time constant, so every slice's load is in flight before the first add (a run-time trip
 // count makes the compiler wait for each load in turn); NS = 0: any split, loads issued eight at a time. The bias
 // values are fetched before the partials. The sum stays 0 + p0 + p1 + ... in ascending z.
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __
   }
 }
 
-// Outputs of 2^30 and more: 64-bit indices and divisions.
+// Partial offsets of 2^31 and more: 64-bit indices and divisions.
 template <typename E, bool kVec>
 __global__ __launch_bounds__(kThreads) void splitk_reduce_wide_kernel(const float* __restrict__ partial,
                                                                       const uint16_t* __restrict__ bias,
@@ -188,6 +189,15 @@ Div30 div30_of(int d) {
   return Div30{unsigned((((1ULL << l) - unsigned(d)) << 32) / unsigned(d) + 1), l};
 }
 
+// The 32-bit kernel forms index partial[z * total + i] (i < total rounded up to a quad) and the magic-number
+// divisions need n < 2^30: both hold when (total + 4) * split < 2^31 and total + 4 < 2^30.
+bool narrow_indices(long long total, int split) {
+  return total + 4 < (1LL << 30) && (total + 4) * static_cast<long long>(split) < (1LL << 31);
+}
+
+// The compile-time slice count of the 32-bit vectorised form (0: any split, loads issued eight at a time).
+int unrolled_split(int split) { return split == 1 || split == 2 || split == 4 || split == 8 ? split : 0; }
+
 template <typename E>
 void launch(const float* partial, const void* bias, void* y, long long total, int split, int M, int HWo, int relu,
             hipStream_t s) {
@@ -196,18 +206,20 @@ void launch(const float* partial, const void* bias, void* y, long long total, in
   const bool vec = (total % 4) == 0 && (reinterpret_cast<uintptr_t>(partial) & 15u) == 0;
   const auto b16 = static_cast<const uint16_t*>(bias);
   const auto y16 = static_cast<uint16_t*>(y);
-  if (total + 4 < (1LL << 30)) {
+  if (narrow_indices(total, split)) {
     const Div30 dh = div30_of(HWo), dm = div30_of(M);
     auto go = [&](auto fn) {
       hipLaunchKernelGGL(fn, dim3(unsigned(blocks)), dim3(kThreads), 0, s, partial, b16, y16, int(total), split, M,
                          HWo, dh, dm, relu);
     };
-    if (!vec) go(splitk_reduce_kernel<E, false, 0>);
-    else if (split == 2) go(splitk_reduce_kernel<E, true, 2>);
-    else if (split == 4) go(splitk_reduce_kernel<E, true, 4>);
-    else if (split == 8) go(splitk_reduce_kernel<E, true, 8>);
-    else if (split == 1) go(splitk_reduce_kernel<E, true, 1>);
-    else go(splitk_reduce_kernel<E, true, 0>);
+    switch (vec ? unrolled_split(split) : -1) {
+      case -1: go(splitk_reduce_kernel<E, false, 0>); break;
+      case 1: go(splitk_reduce_kernel<E, true, 1>); break;
+      case 2: go(splitk_reduce_kernel<E, true, 2>); break;
+      case 4: go(splitk_reduce_kernel<E, true, 4>); break;
+      case 8: go(splitk_reduce_kernel<E, true, 8>); break;
+      default: go(splitk_reduce_kernel<E, true, 0>); break;
+    }
   } else if (vec) {
     hipLaunchKernelGGL((splitk_reduce_wide_kernel<E, true>), dim3(unsigned(blocks)), dim3(kThreads), 0, s, partial,
                        b16, y16, total, split, M, HWo, relu);
@@ -221,6 +233,21 @@ void launch(const float* partial, const void* bias, void* y, long long total, in
 }  // namespace gie_hip
 
 using namespace gie_hip;
+
+extern "C" int gie_hip_splitk_reduce_form(int dtype, int64_t total, int split, int vec, int* index_bits,
+                                          int* slices_unrolled) {
+  if (total <= 0 || split < 1 || !index_bits || !slices_unrolled) return GIE_HIP_EINVAL;
+  if (dtype == GIE_HIP_FP32 || dtype == GIE_HIP_TF32) {
+    *index_bits = 64;
+    *slices_unrolled = 0;
+    return GIE_HIP_OK;
+  }
+  if (dtype != GIE_HIP_FP16 && dtype != GIE_HIP_BF16) return GIE_HIP_EUNSUPPORTED;
+  const bool narrow = narrow_indices(total, split);
+  *index_bits = narrow ? 32 : 64;
+  *slices_unrolled = narrow && vec ? unrolled_split(split) : 0;
+  return GIE_HIP_OK;
+}
 
 extern "C" int gie_hip_splitk_reduce(int dtype, const float* partial, const void* bias, void* y, int64_t total,
                                      int split, int out_channels, int hw_out, int relu, void* stream) {

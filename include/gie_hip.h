@@ -296,6 +296,12 @@ int gie_hip_conv_stack(int config, int dtype, const gie_conv_geom* g, const void
 int gie_hip_splitk_reduce(int dtype, const float* partial, const void* bias, void* y, int64_t total, int split,
                           int out_channels, int hw_out, int relu, void* stream);
 
+/* The kernel form gie_hip_splitk_reduce selects for (dtype, total, split), without launching anything: index_bits =
+   32 when every partial offset z * total + i fits an int (else 64), slices_unrolled = the compile-time slice count
+   of the 32-bit form (1, 2, 4 or 8; 0 = any split). vec != 0 states that total % 4 == 0 and partial is 16-byte
+   aligned. Host-side query for tests and tools; no reference counterpart. */
+int gie_hip_splitk_reduce_form(int dtype, int64_t total, int split, int vec, int* index_bits, int* slices_unrolled);
+
 /* Stand-alone epilogue pass over an NCHW output, in place (the unfused side of the fusion experiment):
    y[i] = round(relu?(f32(y[i]) + f32(bias[(i / hw_out) % out_channels]))); bias may be NULL (ReLU only). dtype
    GIE_HIP_FP32, _FP16 or _BF16; y and bias aligned to their element size. No-op when bias is NULL and relu 0. */

@@ -263,3 +263,29 @@ def test_gather_table_builders_match_oracle(shape):
     with pytest.raises(gie.GieError):
         gie.build_conv_lut(odd, chunked=True)
     assert gie.build_conv_lut(odd).shape == (12 * 9, 4)
+
+
+def test_splitk_reduce_form_keeps_partial_offsets_in_range():
+    """The 32-bit reduce form indexes partial[z * total + i]: it may be chosen only while (total + 4) * split stays
+    below 2^31 (a split-8 reduce over 300M outputs must take the 64-bit form). No launch: the host-side choice."""
+    def form(total, split, vec=1, dtype=gie.PRECISIONS["fp16"]):
+        bits, unrolled = ctypes.c_int(), ctypes.c_int()
+        assert gie.hip().gie_hip_splitk_reduce_form(dtype, total, split, vec, ctypes.byref(bits),
+                                                    ctypes.byref(unrolled)) == 0
+        return bits.value, unrolled.value
+
+    assert form(200_704, 2) == (32, 2)             # config 5 at split 2
+    assert form(200_704, 3) == (32, 0)             # any other split: the run-time slice loop
+    assert form(200_703, 4, vec=0) == (32, 0)      # unaligned: the scalar form
+    for split in (2, 4, 8):
+        limit = (1 << 31) // split - 4             # largest total whose offsets all fit an int
+        assert form(limit - 1, split)[0] == 32
+        assert form(limit, split)[0] == 64
+        assert form(limit + 1000, split)[0] == 64
+    assert form(307_000_000, 8)[0] == 64           # split 8 x 307M outputs: 2.46e9 > 2^31 - 1
+    assert form(716_000_000, 4)[0] == 64
+    assert form((1 << 30) - 4, 1)[0] == 64         # the magic-number divisions need n < 2^30
+    assert form(1000, 4, dtype=gie.PRECISIONS["fp32"]) == (64, 0)
+    bits = ctypes.c_int()
+    assert gie.hip().gie_hip_splitk_reduce_form(gie.PRECISIONS["fp16"], 0, 2, 1, ctypes.byref(bits),
+                                                ctypes.byref(bits)) != 0

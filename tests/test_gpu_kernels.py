@@ -88,7 +88,8 @@ def test_repack_rejects_bad_arguments():
 
 @pytest.mark.parametrize("precision", ["fp16", "bf16"])
 @pytest.mark.parametrize("split,M,HWo,B,relu,yoff", [(2, 512, 49, 8, 1, 0), (8, 512, 49, 8, 1, 2),
-                                                     (4, 7, 13, 3, 0, 0), (3, 5, 9, 1, 1, 2)])
+                                                     (4, 7, 13, 3, 0, 0), (3, 5, 9, 1, 1, 2),
+                                                     (3, 64, 49, 4, 1, 0), (6, 32, 49, 2, 0, 2)])
 def test_splitk_reduce_bit_exact(precision, split, M, HWo, B, relu, yoff):
     total = B * M * HWo
     rng = np.random.default_rng(split * 31 + M)
