@@ -352,17 +352,7 @@ const std::vector<Config>& configs() {
 
 int set_lds_limit(KernelFn fn, int bytes) {
   if (bytes <= 64 * 1024) return GIE_HIP_OK;
-  static std::mutex mu;
-  static std::set<std::pair<const void*, int>> done;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return int(hipErrorInvalidDevice);
-  std::lock_guard<std::mutex> lock(mu);
-  if (done.count({reinterpret_cast<const void*>(fn), dev})) return GIE_HIP_OK;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e != hipSuccess) return int(e);
-  done.insert({reinterpret_cast<const void*>(fn), dev});
-  return GIE_HIP_OK;
+  return lds_opt_in(reinterpret_cast<const void*>(fn), bytes);
 }
 
 }  // namespace

@@ -6,6 +6,9 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "gie_hip.h"
 
@@ -64,6 +67,33 @@ __device__ __forceinline__ uint16_t epilogue(float acc, const uint16_t* __restri
 }
 
 inline int ceil_div_i(long long a, long long b) { return int((a + b - 1) / b); }
+
+// Sets a kernel's dynamic-LDS limit to `bytes` once per (function, device). Each host thread remembers the pairs it
+// has seen set in a small direct-mapped table, so a launch loop takes no lock and touches no shared state; only a
+// thread's first launch of a pair goes through the process-wide set under its mutex.
+inline int lds_opt_in(const void* fn, int bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return int(hipErrorInvalidDevice);
+  struct Seen {
+    const void* fn;
+    int dev;
+  };
+  thread_local Seen seen[16] = {};
+  Seen& slot = seen[((reinterpret_cast<uintptr_t>(fn) >> 8) ^ unsigned(dev)) & 15u];
+  if (slot.fn == fn && slot.dev == dev) return GIE_HIP_OK;
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (!done.count({fn, dev})) {
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+      if (e != hipSuccess) return int(e);
+      done.insert({fn, dev});
+    }
+  }
+  slot = Seen{fn, dev};
+  return GIE_HIP_OK;
+}
 
 // Compute units of the current device, queried once per device and kept (grid sizing on every launch must not
 // pay an attribute query). 256 (MI355X) when the query fails.

@@ -3,8 +3,6 @@
 // themselves, counted waits and the barrier that does not drain prefetches. Private to csrc/kernels.
 #pragma once
 
-#include <mutex>
-#include <set>
 #include <utility>
 
 #include "device_common.h"
@@ -102,21 +100,11 @@ __device__ __forceinline__ unsigned lds_addr(const unsigned char* p) {
   return unsigned(reinterpret_cast<size_t>((__attribute__((address_space(3))) const unsigned char*)p));
 }
 
-// Raises a kernel's dynamic-LDS limit to the whole 160 KiB once per (function, device); launches that need at
-// most 64 KiB skip the call.
+// Raises a kernel's dynamic-LDS limit to the whole 160 KiB once per (function, device) — the largest amount any
+// geometry may use, so one attribute call covers them all; launches that need at most 64 KiB skip the call.
 inline int set_lds_limit(const void* fn, int bytes) {
   if (bytes <= 64 * 1024) return GIE_HIP_OK;
-  static std::mutex mu;
-  static std::set<std::pair<const void*, int>> done;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return int(hipErrorInvalidDevice);
-  std::lock_guard<std::mutex> lock(mu);
-  if (done.count({fn, dev})) return GIE_HIP_OK;
-  // the largest amount any geometry may use, so one attribute call covers them all
-  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  if (e != hipSuccess) return int(e);
-  done.insert({fn, dev});
-  return GIE_HIP_OK;
+  return lds_opt_in(fn, kLdsLimit);
 }
 
 }  // namespace gie_hip

@@ -82,11 +82,13 @@ PlanTable& table() {
   return t;
 }
 
+// The thread's last lookup. It holds its plan weakly: once clear_plan_cache() drops the table's reference, a thread
+// that never calls again does not keep the plan (and the device memory it owns) alive.
 struct LastPlan {
   uint64_t generation = 0;
   PlanRecord record{};
   std::string kernel, cache;
-  std::shared_ptr<ExecutionPlan> plan;
+  std::weak_ptr<ExecutionPlan> plan;
 };
 thread_local LastPlan t_last;
 
@@ -109,7 +111,9 @@ std::shared_ptr<ExecutionPlan> plan_for(const ConvProblem& prob, const Conv2DOpt
   PlanTable& t = table();
   const uint64_t gen = t.generation.load(std::memory_order_acquire);
   LastPlan& last = t_last;
-  if (last.generation == gen && last.record == rec && same_strings(last.kernel, last.cache, opt)) return last.plan;
+  if (last.generation == gen && last.record == rec && same_strings(last.kernel, last.cache, opt)) {
+    if (std::shared_ptr<ExecutionPlan> hit = last.plan.lock()) return hit;
+  }
 
   std::shared_ptr<ExecutionPlan> plan = find_in_table(t, rec, opt);
   if (!plan) {
@@ -121,8 +125,11 @@ std::shared_ptr<ExecutionPlan> plan_for(const ConvProblem& prob, const Conv2DOpt
     for (auto it = range.first; it != range.second && !plan; ++it)
       if (same_strings(it->second.kernel, it->second.cache, opt)) plan = it->second.plan;  // another thread won
     if (!plan) {
-      t.slots.emplace(rec, Slot{opt.kernel, opt.cache_path, built});
       plan = std::move(built);
+      // a clear_plan_cache() that ran while this plan was being built empties the table for good: the plan then
+      // serves this call only and is neither inserted nor remembered
+      if (t.generation.load(std::memory_order_acquire) != gen) return plan;
+      t.slots.emplace(rec, Slot{opt.kernel, opt.cache_path, plan});
     }
   }
   last.generation = gen;

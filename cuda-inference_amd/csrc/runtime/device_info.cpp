@@ -81,8 +81,9 @@ const DeviceInfo& DeviceInfo::get(int device) {
   d.device = device;
   hipDeviceProp_t prop;
   GIE_HIP_CHECK(hipGetDeviceProperties(&prop, device));
-  d.name = prop.name;
   d.gcn_arch = prop.gcnArchName;
+  // some driver stacks leave the marketing name empty: the architecture string then names the device
+  d.name = prop.name[0] != '\0' ? std::string(prop.name) : "AMD GPU " + d.gcn_arch;
   d.cc_major = prop.major;
   d.cc_minor = prop.minor;
   d.global_mem_bytes = prop.totalGlobalMem;
