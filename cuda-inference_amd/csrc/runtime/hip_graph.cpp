@@ -116,6 +116,11 @@ bool HipGraphExecutor::recapture_update(const Enqueue& enqueue) {
   return false;
 }
 
+void HipGraphExecutor::upload(hipStream_t stream) const {
+  GIE_REQUIRE(exec_ != nullptr, StatusCode::kInvalidArgument, "HipGraphExecutor::upload called before capture()");
+  GIE_HIP_CHECK(hipGraphUpload(exec_, stream));
+}
+
 void HipGraphExecutor::launch(hipStream_t stream) const {
   RoctxRange range("gie::HipGraphExecutor::launch");
   GIE_REQUIRE(exec_ != nullptr, StatusCode::kInvalidArgument, "HipGraphExecutor::launch called before capture()");

@@ -1,26 +1,40 @@
-// gie_graph_bench: what a hipGraph buys over eager dispatch for a chain of convolution layers, and what several
-// streams buy for independent convolutions — the measurements of the reference's benchmarks/graph_bench.cpp
-// (cases :58-59, depths :60, record fields :124-139 and :175-184 kept so the two result files line up).
+// gie_graph_bench — launch overhead on one MI355X: what replaying a recorded HIP graph buys over enqueueing the same
+// convolution layers one by one, what several streams buy for independent layers, and what a graph launch itself
+// costs. The questions, the four layer cases and the depth list are those of the reference's
+// benchmarks/graph_bench.cpp (:55-58 cases and depths), and each JSON record carries that program's field names
+// (:120-139, :172-184) so the two result files line up; the program is this build's own.
 //
-// Chain: L layers of one plan ping-ponging between two activation buffers (channels and spatial size preserved),
-//   eager: L ExecutionPlan::execute_unchecked calls per iteration from the host,
-//   graph: one launch of the HipGraphExecutor capture of the same L calls.
-// Per (case, L): capture and instantiate cost, device time per iteration (time_stream_work: event pairs around
-// back-to-back iterations), host enqueue time per iteration (wall clock, no synchronization inside the loop), and
-// whether five graph replays reproduce the eager chain's output bit for bit (input restored before each run).
-// Concurrency: S independent convolutions on one stream vs forked over S streams (default priority) and joined.
+// How it is organised:
+//   * Rig — one layer: its plan, weights, bias, workspace and three activation buffers (the pristine input, and the
+//     two buffers a chain alternates between). chain(stream, L) enqueues L layers; restore() resets the input.
+//   * Probe — every timing: device time per iteration through the library's time_stream_work, host time as the
+//     median over batches of enqueues. When two ways of enqueueing are compared their host batches alternate, so both
+//     see the same machine state (clocks, queue depth, other load).
+//   * Three experiments, each a function returning records: chain (graph vs eager per depth, with a bitwise check of
+//     repeated replays against the eager chain), fanout (S independent layers on one stream vs one stream each, joined
+//     back), and floor (graphs of N empty kernels launched as instantiated, and again after hipGraphUpload, against N
+//     eager empty launches) — the floor separates what a graph launch costs from what the layers cost.
+//   * Output: one JSON record per measurement appended to <out>/graphs.jsonl; with --md FILE the same results as
+//     markdown tables.
 //
-//   gie_graph_bench [--out DIR] [--precision fp16|bf16] [--kernel NAME] [--cases N] [--depths 1,4,16,48]
+//   gie_graph_bench [--out DIR] [--md FILE] [--precision fp16|bf16] [--kernel NAME] [--cases N]
+//                   [--depths 1,4,16,48] [--no-floor]
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
+#include <cstring>
 #include <filesystem>
 #include <fstream>
+#include <iomanip>
+#include <iterator>
 #include <iostream>
+#include <memory>
 #include <sstream>
 #include <string>
 #include <vector>
 
+#include "gie_hip.h"
 #include "gpu_inference/dispatcher.h"
 #include "gpu_inference/execution_plan.h"
 #include "gpu_inference/hip_graph.h"
@@ -32,218 +46,403 @@ using namespace gie;
 
 namespace {
 
-struct ChainCase {
+struct LayerCase {
   const char* name;
   int batch, channels, hw, k;
 };
-const ChainCase kCases[] = {{"b1_c32_14x14_k3", 1, 32, 14, 3},
-                            {"b1_c64_7x7_k1", 1, 64, 7, 1},
-                            {"b1_c64_28x28_k3", 1, 64, 28, 3},
-                            {"b4_c128_14x14_k3", 4, 128, 14, 3}};
+constexpr LayerCase kLayerCases[] = {{"b1_c32_14x14_k3", 1, 32, 14, 3},
+                                     {"b1_c64_7x7_k1", 1, 64, 7, 1},
+                                     {"b1_c64_28x28_k3", 1, 64, 28, 3},
+                                     {"b4_c128_14x14_k3", 4, 128, 14, 3}};
+constexpr int kFanouts[] = {2, 4, 8};
+constexpr int kFloorNodes[] = {1, 4, 16, 64};
 
-// median over 7 rounds of the host wall time per call of `enqueue`, the stream drained between rounds only
-double host_us_per_call(const std::function<void()>& enqueue, hipStream_t s, int calls = 200) {
-  for (int i = 0; i < 20; ++i) enqueue();
-  GIE_HIP_CHECK(hipStreamSynchronize(s));
-  std::vector<double> per_call;
-  for (int round = 0; round < 7; ++round) {
-    const auto t0 = std::chrono::steady_clock::now();
-    for (int i = 0; i < calls; ++i) enqueue();
-    const auto t1 = std::chrono::steady_clock::now();
-    per_call.push_back(std::chrono::duration<double, std::micro>(t1 - t0).count() / calls);
-    GIE_HIP_CHECK(hipStreamSynchronize(s));
+using Enqueue = std::function<void(hipStream_t)>;
+
+// ---- timing ---------------------------------------------------------------------------------------------------------
+
+class Probe {
+ public:
+  explicit Probe(hipStream_t s) : s_(s) {
+    dev_.warmup_iters = 10;
+    dev_.samples = 30;
+    dev_.min_sample_ms = 2.0;
   }
-  return summarize(per_call, 1).median_us;
+
+  // device microseconds per call of `work`, back to back on the stream (median sample)
+  double device_us(const Enqueue& work) const { return time_stream_work(work, s_, dev_).median_us; }
+
+  // host microseconds to enqueue one call of a and of b: batches of each, in alternation, the stream drained after
+  // every batch so queue depth does not build up; median per-call time of each
+  std::pair<double, double> host_us(const Enqueue& a, const Enqueue& b) const {
+    for (int i = 0; i < 16; ++i) {
+      a(s_);
+      b(s_);
+    }
+    drain();
+    std::vector<double> ta, tb;
+    for (int round = 0; round < kRounds; ++round) {
+      ta.push_back(batch_us(a));
+      tb.push_back(batch_us(b));
+    }
+    return {summarize(ta, 1).median_us, summarize(tb, 1).median_us};
+  }
+
+  void drain() const { GIE_HIP_CHECK(hipStreamSynchronize(s_)); }
+  hipStream_t stream() const { return s_; }
+
+ private:
+  static constexpr int kRounds = 9, kCalls = 128;
+  double batch_us(const Enqueue& f) const {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < kCalls; ++i) f(s_);
+    const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+    drain();
+    return us / kCalls;
+  }
+  hipStream_t s_;
+  TimingOptions dev_;
+};
+
+// ---- one layer and its buffers ---------------------------------------------------------------------------------------
+
+class Rig {
+ public:
+  Rig(const ConvProblem& prob, const KernelDesc& kernel, uint64_t seed)
+      : prob_(prob), kernel_(kernel), plan_(ExecutionPlan::create(prob, kernel, 0)),
+        data_(make_conv_data(prob, seed)), bytes_(data_.dy.size()), act_{DeviceBuffer(bytes_), DeviceBuffer(bytes_)},
+        ws_(std::max<size_t>(plan_->workspace_bytes(), 256)) {
+    GIE_REQUIRE(data_.dx.size() == bytes_, StatusCode::kInvalidArgument,
+                "a chain layer must keep its activation shape (same channels in and out, stride 1, same padding)");
+  }
+
+  // layer l reads act_[l % 2] and writes act_[(l + 1) % 2]
+  void chain(hipStream_t s, int layers) const {
+    for (int l = 0; l < layers; ++l)
+      plan_->execute_unchecked(act_[l % 2].data(), data_.dw.data(), data_.db.data(), act_[(l + 1) % 2].data(),
+                               ws_.data(), ws_.size(), s);
+  }
+  // one layer on the rig's own input and output (independent of every other rig)
+  void single(hipStream_t s) const {
+    plan_->execute_unchecked(data_.dx.data(), data_.dw.data(), data_.db.data(), data_.dy.data(), ws_.data(), ws_.size(),
+                             s);
+  }
+  void restore(hipStream_t s) const {
+    GIE_HIP_CHECK(hipMemcpyAsync(act_[0].data(), data_.dx.data(), bytes_, hipMemcpyDeviceToDevice, s));
+  }
+  // raw bytes of a chain's output, after the stream has finished
+  std::vector<unsigned char> result(hipStream_t s, int layers) const {
+    std::vector<unsigned char> h(bytes_);
+    GIE_HIP_CHECK(hipStreamSynchronize(s));
+    GIE_HIP_CHECK(hipMemcpy(h.data(), act_[layers % 2].data(), bytes_, hipMemcpyDeviceToHost));
+    return h;
+  }
+  const ConvProblem& problem() const { return prob_; }
+  const KernelDesc& kernel() const { return kernel_; }
+
+ private:
+  ConvProblem prob_;
+  const KernelDesc& kernel_;
+  std::shared_ptr<ExecutionPlan> plan_;
+  ConvData data_;
+  size_t bytes_;
+  DeviceBuffer act_[2];
+  DeviceBuffer ws_;
+};
+
+ConvProblem problem_of(const LayerCase& c, Precision prec) {
+  ConvProblem p;
+  p.p.batch = c.batch;
+  p.p.in_channels = p.p.out_channels = c.channels;
+  p.p.in_h = p.p.in_w = c.hw;
+  p.p.kernel_h = p.p.kernel_w = c.k;
+  p.p.pad_h = p.p.pad_w = c.k / 2;
+  p.precision = prec;
+  p.has_bias = true;
+  p.activation = Activation::kReLU;
+  return p;
 }
 
-std::vector<unsigned char> bytes_of(const void* dev, size_t n, hipStream_t s) {
-  std::vector<unsigned char> h(n);
-  GIE_HIP_CHECK(hipStreamSynchronize(s));
-  GIE_HIP_CHECK(hipMemcpy(h.data(), dev, n, hipMemcpyDeviceToHost));
-  return h;
+// the named kernel, else the cost model's first choice (no tuning: the question is launch overhead, not the kernel)
+const KernelDesc& kernel_for(const ConvProblem& p, const DeviceInfo& dev, const std::string& forced) {
+  if (!forced.empty()) {
+    const KernelDesc* k = find_kernel(forced);
+    GIE_REQUIRE(k != nullptr, StatusCode::kInvalidArgument, "unknown kernel " + forced);
+    return *k;
+  }
+  const auto ranked = Dispatcher::rank_by_model(p, dev, Dispatcher::compatible_kernels(p, dev));
+  GIE_REQUIRE(!ranked.empty(), StatusCode::kUnsupported, "no kernel for " + p.key());
+  return *ranked.front().first;
 }
 
-std::vector<int> parse_list(const std::string& s) {
-  std::vector<int> v;
-  std::stringstream ss(s);
-  for (std::string item; std::getline(ss, item, ',');)
-    if (!item.empty()) v.push_back(std::stoi(item));
-  return v;
+// ---- experiments -------------------------------------------------------------------------------------------------------
+
+json::Value record(const char* experiment, const DeviceInfo& dev) {
+  json::Value r = json::Value::object();
+  r["experiment"] = experiment;
+  r["gpu"] = dev.name;
+  return r;
 }
 
-TimingOptions chain_timing() {
-  TimingOptions t;
-  t.warmup_iters = 10;
-  t.samples = 30;
-  t.min_sample_ms = 2.0;
-  return t;
+std::vector<json::Value> chain_experiment(const Rig& rig, const std::vector<int>& depths, const Probe& probe,
+                                          const DeviceInfo& dev, const std::string& case_name) {
+  std::vector<json::Value> out;
+  for (const int L : depths) {
+    const Enqueue eager = [&](hipStream_t s) { rig.chain(s, L); };
+    HipGraphExecutor graph;
+    graph.capture(eager);
+    const Enqueue replay = [&](hipStream_t s) { graph.launch(s); };
+
+    // every replay must reproduce the eager chain bit for bit, each from the restored input
+    rig.restore(probe.stream());
+    eager(probe.stream());
+    const std::vector<unsigned char> want = rig.result(probe.stream(), L);
+    bool identical = true;
+    for (int rep = 0; rep < 5; ++rep) {
+      rig.restore(probe.stream());
+      replay(probe.stream());
+      identical = identical && rig.result(probe.stream(), L) == want;
+    }
+
+    const double dev_eager = probe.device_us(eager), dev_graph = probe.device_us(replay);
+    const auto [host_eager, host_graph] = probe.host_us(eager, replay);
+    json::Value r = record("F_hip_graphs", dev);
+    r["case"] = case_name;
+    r["precision"] = to_string(rig.problem().precision);
+    r["kernel"] = rig.kernel().name;
+    r["layers"] = L;
+    r["graph_nodes"] = double(graph.node_count());
+    r["capture_us"] = graph.capture_us();
+    r["instantiate_us"] = graph.instantiate_us();
+    r["eager_device_us"] = dev_eager;
+    r["graph_device_us"] = dev_graph;
+    r["eager_host_launch_us"] = host_eager;
+    r["graph_host_launch_us"] = host_graph;
+    r["device_speedup"] = dev_eager / dev_graph;
+    r["bitwise_identical_replays"] = identical;
+    out.push_back(r);
+  }
+  return out;
+}
+
+// S streams that fan out from a parent stream and join back into it
+class Fanout {
+ public:
+  explicit Fanout(int n) : lanes_(size_t(n)), joined_(size_t(n)) {
+    for (size_t i = 0; i < lanes_.size(); ++i) {
+      GIE_HIP_CHECK(hipStreamCreateWithFlags(&lanes_[i], hipStreamNonBlocking));
+      GIE_HIP_CHECK(hipEventCreateWithFlags(&joined_[i], hipEventDisableTiming));
+    }
+    GIE_HIP_CHECK(hipEventCreateWithFlags(&forked_, hipEventDisableTiming));
+  }
+  ~Fanout() {
+    for (size_t i = 0; i < lanes_.size(); ++i) {
+      (void)hipStreamSynchronize(lanes_[i]);
+      (void)hipEventDestroy(joined_[i]);
+      (void)hipStreamDestroy(lanes_[i]);
+    }
+    (void)hipEventDestroy(forked_);
+  }
+  Fanout(const Fanout&) = delete;
+  Fanout& operator=(const Fanout&) = delete;
+
+  // lane i runs work(i, lane i) after everything already on `parent`; parent continues once every lane is done
+  void run(hipStream_t parent, const std::function<void(int, hipStream_t)>& work) const {
+    GIE_HIP_CHECK(hipEventRecord(forked_, parent));
+    for (size_t i = 0; i < lanes_.size(); ++i) {
+      GIE_HIP_CHECK(hipStreamWaitEvent(lanes_[i], forked_, 0));
+      work(int(i), lanes_[i]);
+      GIE_HIP_CHECK(hipEventRecord(joined_[i], lanes_[i]));
+    }
+    for (hipEvent_t e : joined_) GIE_HIP_CHECK(hipStreamWaitEvent(parent, e, 0));
+  }
+
+ private:
+  std::vector<hipStream_t> lanes_;
+  std::vector<hipEvent_t> joined_;
+  hipEvent_t forked_ = nullptr;
+};
+
+std::vector<json::Value> fanout_experiment(const ConvProblem& prob, const KernelDesc& kernel, const Probe& probe,
+                                           const DeviceInfo& dev, const std::string& case_name) {
+  std::vector<json::Value> out;
+  for (const int S : kFanouts) {
+    std::vector<std::unique_ptr<Rig>> rigs;
+    for (int i = 0; i < S; ++i) rigs.push_back(std::make_unique<Rig>(prob, kernel, 100 + uint64_t(i)));
+    const Fanout fan(S);
+    const Enqueue one_stream = [&](hipStream_t s) {
+      for (const auto& r : rigs) r->single(s);
+    };
+    const Enqueue own_streams = [&](hipStream_t s) { fan.run(s, [&](int i, hipStream_t lane) { rigs[size_t(i)]->single(lane); }); };
+    const double t1 = probe.device_us(one_stream), tn = probe.device_us(own_streams);
+    probe.drain();
+    json::Value r = record("F_stream_concurrency", dev);
+    r["case"] = case_name;
+    r["kernel"] = kernel.name;
+    r["independent_convs"] = S;
+    r["one_stream_us"] = t1;
+    r["multi_stream_us"] = tn;
+    r["speedup"] = t1 / tn;
+    out.push_back(r);
+  }
+  return out;
+}
+
+std::vector<json::Value> floor_experiment(const Probe& probe, const DeviceInfo& dev) {
+  std::vector<json::Value> out;
+  for (const int n : kFloorNodes) {
+    const Enqueue eager = [n](hipStream_t s) {
+      for (int i = 0; i < n; ++i) check_kernel_status(gie_hip_ceiling_empty(s), "empty kernel");
+    };
+    HipGraphExecutor plain, uploaded;
+    plain.capture(eager);
+    uploaded.capture(eager);
+    uploaded.upload(probe.stream());
+    probe.drain();
+    const Enqueue launch_plain = [&](hipStream_t s) { plain.launch(s); };
+    const Enqueue launch_uploaded = [&](hipStream_t s) { uploaded.launch(s); };
+    const auto [host_eager, host_plain] = probe.host_us(eager, launch_plain);
+    const auto [host_eager2, host_uploaded] = probe.host_us(eager, launch_uploaded);
+    json::Value r = record("F_graph_launch_floor", dev);
+    r["empty_kernels"] = n;
+    r["graph_nodes"] = double(plain.node_count());
+    r["eager_host_launch_us"] = 0.5 * (host_eager + host_eager2);
+    r["graph_host_launch_us"] = host_plain;
+    r["uploaded_graph_host_launch_us"] = host_uploaded;
+    r["eager_device_us"] = probe.device_us(eager);
+    r["graph_device_us"] = probe.device_us(launch_plain);
+    r["uploaded_graph_device_us"] = probe.device_us(launch_uploaded);
+    out.push_back(r);
+  }
+  return out;
+}
+
+// ---- reporting ---------------------------------------------------------------------------------------------------------
+
+std::string fmt(double v, int digits = 1) {
+  std::ostringstream o;
+  o << std::fixed << std::setprecision(digits) << v;
+  return o.str();
+}
+
+std::string markdown(const std::vector<json::Value>& rows) {
+  std::ostringstream md;
+  auto num = [](const json::Value& r, const char* k) { return r.find(k) ? r.find(k)->as_double() : 0.0; };
+  auto str = [](const json::Value& r, const char* k) { return r.find(k) ? r.find(k)->as_string() : std::string(); };
+  auto of = [&](const char* experiment) {
+    std::vector<const json::Value*> v;
+    for (const auto& r : rows)
+      if (str(r, "experiment") == experiment) v.push_back(&r);
+    return v;
+  };
+  if (const auto f = of("F_graph_launch_floor"); !f.empty()) {
+    md << "| empty kernels | graph nodes | host µs eager → graph → uploaded graph | device µs eager → graph → "
+          "uploaded graph |\n|---|---|---|---|\n";
+    for (const json::Value* r : f)
+      md << "| " << num(*r, "empty_kernels") << " | " << num(*r, "graph_nodes") << " | "
+         << fmt(num(*r, "eager_host_launch_us")) << " → " << fmt(num(*r, "graph_host_launch_us")) << " → "
+         << fmt(num(*r, "uploaded_graph_host_launch_us")) << " | " << fmt(num(*r, "eager_device_us")) << " → "
+         << fmt(num(*r, "graph_device_us")) << " → " << fmt(num(*r, "uploaded_graph_device_us")) << " |\n";
+    md << "\n";
+  }
+  if (const auto c = of("F_hip_graphs"); !c.empty()) {
+    md << "| case | kernel | L | eager device µs | graph device µs | speedup | host µs eager → graph | capture + "
+          "instantiate µs | replays bitwise |\n|---|---|---|---|---|---|---|---|---|\n";
+    for (const json::Value* r : c)
+      md << "| " << str(*r, "case") << " | `" << str(*r, "kernel") << "` | " << num(*r, "layers") << " | "
+         << fmt(num(*r, "eager_device_us")) << " | " << fmt(num(*r, "graph_device_us")) << " | "
+         << fmt(num(*r, "device_speedup"), 2) << " | " << fmt(num(*r, "eager_host_launch_us")) << " → "
+         << fmt(num(*r, "graph_host_launch_us")) << " | " << fmt(num(*r, "capture_us"), 0) << " + "
+         << fmt(num(*r, "instantiate_us"), 0) << " | "
+         << (r->find("bitwise_identical_replays")->as_bool() ? "yes" : "NO") << " |\n";
+    md << "\n";
+  }
+  if (const auto s = of("F_stream_concurrency"); !s.empty()) {
+    md << "| case | independent convs S | one stream µs | S streams µs | speedup |\n|---|---|---|---|---|\n";
+    for (const json::Value* r : s)
+      md << "| " << str(*r, "case") << " | " << num(*r, "independent_convs") << " | " << fmt(num(*r, "one_stream_us"))
+         << " | " << fmt(num(*r, "multi_stream_us")) << " | " << fmt(num(*r, "speedup"), 2) << " |\n";
+  }
+  return md.str();
+}
+
+struct Args {
+  std::string out_dir = "results/graphs", md_path, kernel;
+  Precision precision = Precision::kFp16;
+  int cases = int(std::size(kLayerCases));
+  std::vector<int> depths = {1, 4, 16, 48};
+  bool floor = true;
+};
+
+Args parse(int argc, char** argv) {
+  Args a;
+  for (int i = 1; i < argc; ++i) {
+    const std::string opt = argv[i];
+    const auto value = [&]() -> std::string {
+      GIE_REQUIRE(i + 1 < argc, StatusCode::kInvalidArgument, opt + " needs a value");
+      return argv[++i];
+    };
+    if (opt == "--out") {
+      a.out_dir = value();
+    } else if (opt == "--md") {
+      a.md_path = value();
+    } else if (opt == "--precision") {
+      a.precision = precision_from_string(value());
+    } else if (opt == "--kernel") {
+      a.kernel = value();
+    } else if (opt == "--cases") {
+      a.cases = std::clamp(std::stoi(value()), 1, int(std::size(kLayerCases)));
+    } else if (opt == "--depths") {
+      a.depths.clear();
+      std::stringstream list(value());
+      for (std::string d; std::getline(list, d, ',');)
+        if (!d.empty()) a.depths.push_back(std::stoi(d));
+    } else if (opt == "--no-floor") {
+      a.floor = false;
+    } else {
+      throw Error(StatusCode::kInvalidArgument, "unknown option " + opt);
+    }
+  }
+  return a;
 }
 
 }  // namespace
 
 int main(int argc, char** argv) {
   try {
-    std::string out_dir = "results/graphs", kernel_name;
-    Precision prec = Precision::kFp16;
-    int n_cases = int(sizeof(kCases) / sizeof(kCases[0]));
-    std::vector<int> depths = {1, 4, 16, 48};
-    for (int i = 1; i < argc; ++i) {
-      const std::string a = argv[i];
-      auto next = [&]() -> std::string {
-        if (i + 1 >= argc) throw Error(StatusCode::kInvalidArgument, a + " needs a value");
-        return argv[++i];
-      };
-      if (a == "--out") out_dir = next();
-      else if (a == "--precision") prec = precision_from_string(next());
-      else if (a == "--kernel") kernel_name = next();
-      else if (a == "--cases") n_cases = std::min(n_cases, std::max(1, std::stoi(next())));
-      else if (a == "--depths") depths = parse_list(next());
-      else throw Error(StatusCode::kInvalidArgument, "unknown option " + a);
-    }
+    const Args args = parse(argc, argv);
     GIE_HIP_CHECK(hipSetDevice(0));
     const DeviceInfo& dev = DeviceInfo::get(0);
-    std::filesystem::create_directories(out_dir);
-    std::ofstream out(out_dir + "/graphs.jsonl", std::ios::app);
+    std::filesystem::create_directories(args.out_dir);
+    std::ofstream jsonl(args.out_dir + "/graphs.jsonl", std::ios::app);
     hipStream_t stream = nullptr;
     GIE_HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
-
-    for (int ci = 0; ci < n_cases; ++ci) {
-      const ChainCase& c = kCases[ci];
-      ConvProblem prob;
-      prob.p.batch = c.batch;
-      prob.p.in_channels = prob.p.out_channels = c.channels;
-      prob.p.in_h = prob.p.in_w = c.hw;
-      prob.p.kernel_h = prob.p.kernel_w = c.k;
-      prob.p.pad_h = prob.p.pad_w = c.k / 2;
-      prob.precision = prec;
-      prob.has_bias = true;
-      prob.activation = Activation::kReLU;
-      // the kernel: named, else the cost model's first choice (no tuning, as the reference's bench)
-      const KernelDesc* k = kernel_name.empty() ? nullptr : find_kernel(kernel_name);
-      if (!kernel_name.empty() && k == nullptr) throw Error(StatusCode::kInvalidArgument, "no kernel " + kernel_name);
-      if (k == nullptr) {
-        const auto cands = Dispatcher::compatible_kernels(prob, dev);
-        if (cands.empty()) throw Error(StatusCode::kUnsupported, "no kernel runs " + prob.key());
-        k = Dispatcher::rank_by_model(prob, dev, cands).front().first;
-      }
-      const std::shared_ptr<ExecutionPlan> plan = ExecutionPlan::create(prob, *k, 0);
-      ConvData d = make_conv_data(prob, 11);
-      const size_t act_bytes = d.dy.size();  // == d.dx.size(): the layer preserves the activation shape
-      DeviceBuffer ping(act_bytes), pong(act_bytes), ws(plan->workspace_bytes());
-
-      for (int depth : depths) {
-        auto chain = [&](hipStream_t s) {
-          const void* src = ping.data();
-          void* dst = pong.data();
-          for (int l = 0; l < depth; ++l) {
-            plan->execute_unchecked(src, d.dw.data(), d.db.data(), dst, ws.data(), ws.size(), s);
-            const void* prev_dst = dst;
-            dst = const_cast<void*>(src);
-            src = prev_dst;
-          }
-        };
-        void* last = depth % 2 == 1 ? pong.data() : ping.data();  // buffer the last layer writes
-        auto restore_input = [&]() {
-          GIE_HIP_CHECK(hipMemcpyAsync(ping.data(), d.dx.data(), act_bytes, hipMemcpyDeviceToDevice, stream));
-        };
-        HipGraphExecutor graph;
-        graph.capture(chain);
-
-        restore_input();
-        chain(stream);
-        const std::vector<unsigned char> eager_out = bytes_of(last, act_bytes, stream);
-        bool identical = true;
-        for (int rep = 0; rep < 5; ++rep) {
-          restore_input();
-          graph.launch(stream);
-          identical = identical && bytes_of(last, act_bytes, stream) == eager_out;
+    std::vector<json::Value> all;
+    {
+      const Probe probe(stream);
+      auto emit = [&](std::vector<json::Value> rows) {
+        for (json::Value& r : rows) {
+          jsonl << r.dump() << "\n";
+          std::cout << r.dump() << "\n";
+          all.push_back(std::move(r));
         }
-
-        const TimingStats te = time_stream_work(chain, stream, chain_timing());
-        const TimingStats tg = time_stream_work([&](hipStream_t s) { graph.launch(s); }, stream, chain_timing());
-        const double he = host_us_per_call([&] { chain(stream); }, stream);
-        const double hg = host_us_per_call([&] { graph.launch(stream); }, stream);
-
-        json::Value r = json::Value::object();
-        r["experiment"] = "F_hip_graphs";
-        r["gpu"] = dev.name;
-        r["case"] = c.name;
-        r["precision"] = to_string(prec);
-        r["kernel"] = k->name;
-        r["layers"] = depth;
-        r["graph_nodes"] = double(graph.node_count());
-        r["capture_us"] = graph.capture_us();
-        r["instantiate_us"] = graph.instantiate_us();
-        r["eager_device_us"] = te.median_us;
-        r["graph_device_us"] = tg.median_us;
-        r["eager_host_launch_us"] = he;
-        r["graph_host_launch_us"] = hg;
-        r["device_speedup"] = te.median_us / tg.median_us;
-        r["bitwise_identical_replays"] = identical;
-        out << r.dump() << "\n";
-        out.flush();
-        std::cout << c.name << " L=" << depth << " [" << k->name << "] eager " << te.median_us << " us, graph "
-                  << tg.median_us << " us (x" << te.median_us / tg.median_us << "), host " << he << " -> " << hg
-                  << " us, identical=" << identical << std::endl;
+        jsonl.flush();
+        std::cout.flush();
+      };
+      if (args.floor) emit(floor_experiment(probe, dev));
+      for (int ci = 0; ci < args.cases; ++ci) {
+        const ConvProblem prob = problem_of(kLayerCases[ci], args.precision);
+        const KernelDesc& kernel = kernel_for(prob, dev, args.kernel);
+        const Rig rig(prob, kernel, 11);
+        emit(chain_experiment(rig, args.depths, probe, dev, kLayerCases[ci].name));
+        emit(fanout_experiment(prob, kernel, probe, dev, kLayerCases[ci].name));
       }
-
-      // S independent copies of the layer: one stream back to back vs one stream each, forked and joined by events
-      for (int S : {2, 4, 8}) {
-        std::vector<ConvData> data;
-        std::vector<DeviceBuffer> wss;
-        std::vector<hipStream_t> side(static_cast<size_t>(S));
-        std::vector<hipEvent_t> joined(static_cast<size_t>(S));
-        for (int s = 0; s < S; ++s) {
-          data.push_back(make_conv_data(prob, 100 + uint64_t(s)));
-          wss.emplace_back(plan->workspace_bytes());
-          GIE_HIP_CHECK(hipStreamCreateWithFlags(&side[size_t(s)], hipStreamNonBlocking));
-          GIE_HIP_CHECK(hipEventCreateWithFlags(&joined[size_t(s)], hipEventDisableTiming));
-        }
-        hipEvent_t forked = nullptr;
-        GIE_HIP_CHECK(hipEventCreateWithFlags(&forked, hipEventDisableTiming));
-        auto conv = [&](int s, hipStream_t st) {
-          const ConvData& cd = data[size_t(s)];
-          plan->execute_unchecked(cd.dx.data(), cd.dw.data(), cd.db.data(), cd.dy.data(), wss[size_t(s)].data(),
-                                  wss[size_t(s)].size(), st);
-        };
-        auto one_stream = [&](hipStream_t st) {
-          for (int s = 0; s < S; ++s) conv(s, st);
-        };
-        auto many_streams = [&](hipStream_t st) {
-          GIE_HIP_CHECK(hipEventRecord(forked, st));
-          for (int s = 0; s < S; ++s) {
-            GIE_HIP_CHECK(hipStreamWaitEvent(side[size_t(s)], forked, 0));
-            conv(s, side[size_t(s)]);
-            GIE_HIP_CHECK(hipEventRecord(joined[size_t(s)], side[size_t(s)]));
-          }
-          for (int s = 0; s < S; ++s) GIE_HIP_CHECK(hipStreamWaitEvent(st, joined[size_t(s)], 0));
-        };
-        const TimingStats t1 = time_stream_work(one_stream, stream, chain_timing());
-        const TimingStats tn = time_stream_work(many_streams, stream, chain_timing());
-        GIE_HIP_CHECK(hipStreamSynchronize(stream));
-        json::Value r = json::Value::object();
-        r["experiment"] = "F_stream_concurrency";
-        r["gpu"] = dev.name;
-        r["case"] = c.name;
-        r["kernel"] = k->name;
-        r["independent_convs"] = S;
-        r["one_stream_us"] = t1.median_us;
-        r["multi_stream_us"] = tn.median_us;
-        r["speedup"] = t1.median_us / tn.median_us;
-        out << r.dump() << "\n";
-        out.flush();
-        std::cout << c.name << " " << S << " independent convs: 1 stream " << t1.median_us << " us, " << S
-                  << " streams " << tn.median_us << " us (x" << t1.median_us / tn.median_us << ")" << std::endl;
-        for (int s = 0; s < S; ++s) {
-          (void)hipStreamDestroy(side[size_t(s)]);
-          (void)hipEventDestroy(joined[size_t(s)]);
-        }
-        (void)hipEventDestroy(forked);
-      }
+      probe.drain();
     }
-    (void)hipStreamDestroy(stream);
+    if (!args.md_path.empty()) std::ofstream(args.md_path) << markdown(all);
+    GIE_HIP_CHECK(hipStreamDestroy(stream));
   } catch (const std::exception& e) {
-    std::cerr << "error: " << e.what() << "\n";
+    std::cerr << "gie_graph_bench: " << e.what() << "\n";
     return 1;
   }
   return 0;

@@ -26,6 +26,9 @@ class HipGraphExecutor {
   // Returns true if updated in place.
   bool recapture_update(const Enqueue& enqueue);
   void launch(hipStream_t stream) const;
+  // Uploads the executable graph's device-side state on `stream` ahead of the first launch (hipGraphUpload), so
+  // that launch does not pay for it. Addition to the reference's interface.
+  void upload(hipStream_t stream) const;
 
   bool valid() const { return exec_ != nullptr; }
   size_t node_count() const { return nodes_; }
