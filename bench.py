@@ -16,6 +16,7 @@ on the same quantized inputs, timed on this host.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -90,6 +91,9 @@ def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
     us_call = ms * 1e3 / steps
     flops = p.flops()
     tflops = flops / (us_call * 1e-6) / 1e12
+    # the reference harness's protocol (benchmark_main.cpp:55-56, timing.cpp:42-83): warm-up 5, then 30 samples of
+    # back-to-back forward calls lasting >= 1 ms each, median per call
+    med = gie.time_forward(p, t, ws, stream, warmup=5, samples=30, min_sample_ms=1.0, **opts)
     # per-stage device time (events on the launch stream around each kernel), same plan and buffers
     plan = gie.Plan(p, kernel)
     stages = plan.time_stages(t, ws, stream, iters=max(50, min(steps, 400)))
@@ -104,6 +108,10 @@ def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
     out = {
         "kernel": kernel, "selection": source, "gemm_view": {"M": p.gemm_m, "N": p.gemm_n, "K": p.gemm_k},
         "gflop": flops / 1e9, "us_per_call": us_call, "tflops": tflops,
+        "median_protocol": {"us_per_call": med["median_us"], "tflops": flops / (med["median_us"] * 1e-6) / 1e12,
+                            "p10_us": med["p10_us"], "p90_us": med["p90_us"], "calls_per_sample": med["inner"],
+                            "samples": med["samples"], "warmup": med["warmup"],
+                            "min_sample_ms": med["min_sample_ms"]},
         "pct_of_fp16_peak": 100.0 * tflops / PEAK_FP16_TFLOPS,
         "roofline_tflops": roof_tflops, "roofline_fraction": tflops / roof_tflops,
         "bound": "mfma" if ai * PEAK_HBM_GBS / 1e3 >= PEAK_FP16_TFLOPS else "hbm",
@@ -139,6 +147,45 @@ def reduce_bytes(split: int, p):
         return None
     ny = float(np.prod(p.y_shape()))
     return split * ny * 4 + ny * p.esize + p.out_channels * p.esize
+
+
+def repack_rates(gie, cfg, stream, launches: int = 200):
+    """Achieved HBM rate of the repack kernels on one config's tensors: the NCHW -> NHWC activation repack, the
+    OIHW -> O.RS.C weight repack (channels padded to a multiple of 8, as the implicit-GEMM entries use them) and the
+    two in one dispatch, each launched `launches` times back to back between two events on the bench stream.
+    Bytes = elements read (unpadded) + elements written (padded), 2 bytes each."""
+    p = gie.Problem(**cfg, has_bias=True, relu=True)
+    x, w, b = gie.make_host_data(p, SEED, "uniform", "benchmark")
+    cp = (p.in_channels + 7) // 8 * 8
+    hw, rs = p.in_h * p.in_w, p.kernel_h * p.kernel_w
+    nx, nw = p.batch * p.in_channels * hw, p.out_channels * p.in_channels * rs
+    nxp, nwp = p.batch * hw * cp, p.out_channels * rs * cp
+    dx, dw = gie.to_device(gie.host_to_storage(x, p.precision)), gie.to_device(gie.host_to_storage(w, p.precision))
+    dxn, dwk = gie.DeviceBuffer(2 * nxp + 256), gie.DeviceBuffer(2 * nwp + 256)
+    g = p.geom(cp)
+    H = gie.hip()
+    kernels = {
+        "act_nchw_to_nhwc": (lambda: H.gie_hip_repack_act_nchw_to_nhwc(dx.addr, dxn.addr, p.batch, p.in_channels, hw,
+                                                                       cp, stream.h), 2 * (nx + nxp)),
+        "w_oihw_to_orsc": (lambda: H.gie_hip_repack_w_oihw_to_orsc(dw.addr, dwk.addr, p.out_channels, p.in_channels,
+                                                                   rs, cp, stream.h), 2 * (nw + nwp)),
+        "act_and_w_one_dispatch": (lambda: H.gie_hip_repack_act_and_w(dx.addr, dxn.addr, dw.addr, dwk.addr,
+                                                                      ctypes.byref(g), stream.h),
+                                   2 * (nx + nxp + nw + nwp)),
+    }
+    out = {}
+    for name, (launch, nbytes) in kernels.items():
+        for _ in range(20):
+            gie.check_hip(launch(), name)
+        e0, e1 = gie.Event(), gie.Event()
+        e0.record(stream)
+        for _ in range(launches):
+            gie.check_hip(launch(), name)
+        e1.record(stream)
+        e1.sync()
+        us = e0.elapsed_ms(e1) * 1e3 / launches
+        out[name] = {"us_per_launch": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
+    return out
 
 
 def fastest_split_entry(gie, cfg, stream):
@@ -317,8 +364,8 @@ def main():
         p, t, r = run_config(gie, name, CONFIGS[name], steps, args.warmup if name == HEADLINE else 50, stream,
                              args.tune_cache, args.kernel if name == HEADLINE else None)
         log(f"[bench] {name}: {r['kernel']} {r['us_per_call']:.2f} us/call {r['tflops']:.1f} TFLOP/s "
-            f"(gemm {r['stage_us']['gemm_us']:.2f} us, repack {r['stage_us']['repack_us']:.2f} us) "
-            f"rel_l2={r['rel_l2']:.2e}")
+            f"(median protocol {r['median_protocol']['us_per_call']:.2f} us; gemm {r['stage_us']['gemm_us']:.2f} us, "
+            f"repack {r['stage_us']['repack_us']:.2f} us) rel_l2={r['rel_l2']:.2e}")
         results[name] = r
         if name == HEADLINE:
             head = (p, t)
@@ -334,6 +381,16 @@ def main():
             log(f"[bench] {SPLITK} split-K: {r['kernel']} {r['us_per_call']:.2f} us/call, reduce "
                 f"{r['stage_us']['reduce_us']:.2f} us = {r['reduce_gbs'] or 0:.0f} GB/s")
             results[SPLITK + "_forced_splitk"] = r
+    repack = {}
+    if not args.kernel:
+        # the repack kernels of the implicit-GEMM path, on the configs whose tensors they would move
+        for name in names:
+            repack[name] = repack_rates(gie, CONFIGS[name], stream)
+            r = repack[name]
+            log(f"[bench] {name} repack: activations {r['act_nchw_to_nhwc']['gbs']:.0f} GB/s "
+                f"({r['act_nchw_to_nhwc']['us_per_launch']:.2f} us), weights {r['w_oihw_to_orsc']['gbs']:.0f} GB/s "
+                f"({r['w_oihw_to_orsc']['us_per_launch']:.2f} us), both in one dispatch "
+                f"{r['act_and_w_one_dispatch']['gbs']:.0f} GB/s")
     hr = results[HEADLINE]
     p, t = head
     cpu = None
@@ -355,7 +412,9 @@ def main():
         "dtype": "fp16", "data": "synthetic (SplitMix64 seed 0x1234ABCD; x U[-1,1], w U[-1,1]/sqrt(K), b U[-0.1,0.1])",
         "config": {"workload": "BASELINE configs[1]: FP16 NCHW 3x3 conv N=32 C=256 H=W=14 K=256 s1 p1 + bias + ReLU",
                    "gemm_view": hr["gemm_view"], "kernel": hr["kernel"], "selection": hr["selection"],
-                   "pct_of_fp16_peak": hr["pct_of_fp16_peak"], "us_per_call": hr["us_per_call"]},
+                   "pct_of_fp16_peak": hr["pct_of_fp16_peak"], "us_per_call": hr["us_per_call"],
+                   "median_protocol_us_per_call": hr["median_protocol"]["us_per_call"],
+                   "median_protocol_tflops": hr["median_protocol"]["tflops"]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_FP16_TFLOPS, "traffic": load_traffic(hr["kernel"]),
                      "kernel": dominant_kernel(hr["kernel"]), "avg_launch_us": gemm_us,
@@ -365,6 +424,7 @@ def main():
         "parity": {"rel_l2": hr["rel_l2"], "max_abs": hr["max_abs"], "ok": hr["parity_ok"],
                    "against": "library GPU double reference on the timed call's inputs"},
         "configs": results,
+        "repack_kernels": repack,
     }
     print(json.dumps(line), flush=True)
 

@@ -216,6 +216,29 @@ int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_te
   });
 }
 
+int gie_conv2d_time_forward(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                            const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
+                            const gie_options* opt, int warmup, int samples, double min_sample_ms, double* stats7,
+                            int* inner) {
+  return guarded([&] {
+    const ConstTensorRef b = bias ? to_cref(bias) : ConstTensorRef{};
+    const ConstTensorRef xr = to_cref(x), wr = to_cref(w);
+    const TensorRef yr = to_ref(y);
+    const ConvProblem pr = to_problem(p);
+    const Conv2DOptions o = to_options(opt);
+    TimingOptions to;
+    to.warmup_iters = warmup;
+    to.samples = samples;
+    to.min_sample_ms = min_sample_ms;
+    const TimingStats t = time_stream_work(
+        [&](hipStream_t s) { Conv2D::forward(xr, wr, bias ? &b : nullptr, pr, yr, workspace, workspace_bytes, s, o); },
+        static_cast<hipStream_t>(stream), to);
+    const double v[7] = {t.median_us, t.mean_us, t.min_us, t.max_us, t.p10_us, t.p90_us, t.stddev_us};
+    if (stats7) std::memcpy(stats7, v, sizeof(v));
+    if (inner) *inner = t.inner_iters;
+  });
+}
+
 int gie_measure_host_cost(const gie_problem* p, const gie_options* opt, int batch, double* out3) {
   return guarded([&] {
     GIE_REQUIRE(p != nullptr && out3 != nullptr && batch > 0, StatusCode::kInvalidArgument,

@@ -110,6 +110,8 @@ _CAPI = {
     "gie_problem_key": ([_PP, _cp, _sz], _i),
     "gie_conv2d_forward": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP], _i),
     "gie_conv2d_forward_n": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP, _i], _i),
+    "gie_conv2d_time_forward": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP, _i, _i, ctypes.c_double,
+                                 ctypes.POINTER(ctypes.c_double), _ip], _i),
     "gie_conv2d_workspace_size": ([_PP, _OP, ctypes.POINTER(_sz)], _i),
     "gie_make_host_data": ([_PP, ctypes.c_uint64, _i, _i, _vp, _vp, _vp], _i),
     "gie_conv2d_clear_plan_cache": ([], _i),
@@ -201,6 +203,7 @@ _HIP = {
     "gie_hip_pw_check": ([_GP, _ip], _i),
     "gie_hip_conv_pw": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_splitk_reduce": ([_i, _vp, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _vp], _i),
+    "gie_hip_splitk_reduce_form": ([_i, ctypes.c_int64, _i, _i, _ip, _ip], _i),
     "gie_hip_bias_act": ([_i, _vp, _vp, ctypes.c_int64, _i, _i, _i, _vp], _i),
     "gie_hip_pws_check": ([_GP, _vp], _i),
     "gie_hip_conv_pws": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
@@ -547,6 +550,22 @@ def forward_n(p: Problem, t: ConvTensors, workspace: DeviceBuffer | None, stream
                                       ctypes.byref(b) if b is not None else None, ctypes.byref(y),
                                       workspace.addr if workspace else None, workspace.nbytes if workspace else 0,
                                       stream.h if stream else None, ctypes.byref(oc), count), "Conv2D::forward x n")
+
+
+def time_forward(p: Problem, t: ConvTensors, workspace: DeviceBuffer | None, stream: Stream | None, warmup=5,
+                 samples=30, min_sample_ms=1.0, **opt) -> dict:
+    """Conv2D::forward under the library's time_stream_work protocol (warm-up, then `samples` samples of
+    back-to-back calls lasting >= min_sample_ms each): per-call microsecond statistics."""
+    pc, oc = p.c(), _opts(**opt)
+    x, w, b, y = t.tensors()
+    st, inner = (ctypes.c_double * 7)(), ctypes.c_int()
+    check(capi().gie_conv2d_time_forward(ctypes.byref(pc), ctypes.byref(x), ctypes.byref(w),
+                                         ctypes.byref(b) if b is not None else None, ctypes.byref(y),
+                                         workspace.addr if workspace else None, workspace.nbytes if workspace else 0,
+                                         stream.h if stream else None, ctypes.byref(oc), warmup, samples,
+                                         min_sample_ms, st, ctypes.byref(inner)), "Conv2D::forward timing")
+    keys = ("median_us", "mean_us", "min_us", "max_us", "p10_us", "p90_us", "stddev_us")
+    return dict(zip(keys, list(st)), inner=inner.value, samples=samples, warmup=warmup, min_sample_ms=min_sample_ms)
 
 
 def measure_host_cost(p: Problem, batch: int = 256, **opt) -> dict:

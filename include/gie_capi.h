@@ -55,6 +55,14 @@ int gie_conv2d_forward(const gie_problem* p, const gie_tensor* x, const gie_tens
 int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
                          const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
                          const gie_options* opt, int count);
+/* time_stream_work (timing.h:36-38, the reference's timing.cpp:42-83 protocol) around Conv2D::forward itself:
+   `warmup` calls, then `samples` samples of back-to-back forward calls lasting at least min_sample_ms each;
+   stats = {median, mean, min, max, p10, p90, stddev} in microseconds per call, *inner = calls per sample. The
+   reference's benchmark harness reports the median of this protocol (benchmarks/benchmark_main.cpp:55-56). */
+int gie_conv2d_time_forward(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
+                            const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
+                            const gie_options* opt, int warmup, int samples, double min_sample_ms, double* stats7,
+                            int* inner);
 /* Host cost of the plan API, no counterpart in the reference: median host wall time to enqueue one
    gie_conv2d_forward call on problem p (zero-filled tensors, plan already cached) and one bare empty-kernel launch,
    each over batches of `batch` back-to-back calls; out3 = {host us per forward, host us per bare launch,
