@@ -133,6 +133,54 @@ constexpr int kDma4 = 1, kReg2 = 2;
 // PADS_LOADED: the padding columns of the LDS rows hold whatever the row loads brought in (16-byte loads run past
 // the row end into them); the left neighbour of column 0 and the right neighbour of column W - 1 are padding, so those
 // two shifted terms are selected out instead of read as zeros.
+// Block j of a unit's output: the three tap-column accumulator sets shifted into place and added.
+template <int P, int NBW, bool PADS_LOADED>
+__device__ __forceinline__ f32x4 slab_column(const f32x4 (&acc)[3][NBW], int j, int lane, int wr, int W) {
+  constexpr int RW = 16 * NBW / P;
+  if constexpr (PADS_LOADED && P == 16) {
+    // a 16-position block is one row: the cross-block terms reach only column 0 (its left neighbour is padding)
+    // and column 15 (never stored), and the row shift already gives column 0 nothing; only the right neighbour of
+    // column W - 1, position W, has to be zeroed before the shift
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 a2 = (lane & 15) == W ? zero : acc[2][j];
+    return acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(a2);
+  } else if constexpr (PADS_LOADED) {
+    f32x4 t0 = dpp4<kShr1>(acc[0][j]), t2 = dpp4<kShl1>(acc[2][j]);
+    if (j > 0) t0 += dpp4<kShl15>(acc[0][j - 1]);
+    if (j + 1 < NBW) t2 += dpp4<kShr15>(acc[2][j + 1]);
+    const int c = (wr * RW * P + 16 * j + (lane & 15)) % P;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    return acc[1][j] + (c != 0 ? t0 : zero) + (c != W - 1 ? t2 : zero);
+  } else {
+    f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
+    if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
+    if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
+    return out;
+  }
+}
+
+// Bias + ReLU + one rounding of a lane's four filters at one position, then the pixel-pair exchange between lane
+// pairs: the even lane (column c) ends with filters 0 and 1 at columns (c, c + 1), the odd lane with filters 2 and 3
+// at columns (c - 1, c), each as one 4-byte word (low half = the left column).
+template <typename E>
+__device__ __forceinline__ void round_pairs(const f32x4& out, const float (&bv)[4], int relu, uint32_t oddm,
+                                            uint32_t* wa, uint32_t* wb) {
+  uint32_t h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v = out[i] + bv[i];
+    h[i] = E::from_f32(relu ? fmaxf(v, 0.0f) : v);
+  }
+  const uint32_t lo01 = h[0] | (h[1] << 16), lo23 = h[2] | (h[3] << 16);
+  const uint32_t send = (lo01 & oddm) | (lo23 & ~oddm);
+  const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap lane pairs
+  // even: (h0, recv.lo) and (h1, recv.hi); odd: (recv.lo, h2) and (recv.hi, h3)
+  const uint32_t wa_e = (h[0] & 0xffffu) | (recv << 16), wb_e = (h[1] & 0xffffu) | (recv & 0xffff0000u);
+  const uint32_t wa_o = (recv & 0xffffu) | (h[2] << 16), wb_o = (recv >> 16) | (h[3] << 16);
+  *wa = (wa_o & oddm) | (wa_e & ~oddm);
+  *wb = (wb_o & oddm) | (wb_e & ~oddm);
+}
+
 template <typename E, int P, int NBW, bool PADS_LOADED = false>
 __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uint32_t (&bbits)[4], int lane, int wr,
                                            int oh0, int nrows, int b, int z, int o0, int f0,
@@ -140,26 +188,7 @@ __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uin
   constexpr int RW = 16 * NBW / P;
   (void)o0;
   auto column = [&](int j) __attribute__((always_inline)) {
-    if constexpr (PADS_LOADED && P == 16) {
-      // a 16-position block is one row: the cross-block terms reach only column 0 (its left neighbour is padding)
-      // and column 15 (never stored), and the row shift already gives column 0 nothing; only the right neighbour of
-      // column W - 1, position W, has to be zeroed before the shift
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      const f32x4 a2 = (lane & 15) == g.W ? zero : acc[2][j];
-      return acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(a2);
-    } else if constexpr (PADS_LOADED) {
-      f32x4 t0 = dpp4<kShr1>(acc[0][j]), t2 = dpp4<kShl1>(acc[2][j]);
-      if (j > 0) t0 += dpp4<kShl15>(acc[0][j - 1]);
-      if (j + 1 < NBW) t2 += dpp4<kShr15>(acc[2][j + 1]);
-      const int c = (wr * RW * P + 16 * j + (lane & 15)) % P;
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      return acc[1][j] + (c != 0 ? t0 : zero) + (c != g.W - 1 ? t2 : zero);
-    } else {
-      f32x4 out = acc[1][j] + dpp4<kShr1>(acc[0][j]) + dpp4<kShl1>(acc[2][j]);
-      if (j > 0) out += dpp4<kShl15>(acc[0][j - 1]);
-      if (j + 1 < NBW) out += dpp4<kShr15>(acc[2][j + 1]);
-      return out;
-    }
+    return slab_column<P, NBW, PADS_LOADED>(acc, j, lane, wr, g.W);
   };
   const int nf = g.O - f0;                         // filters of the lane's four that exist (>= 4: all)
   const int fbase = (b * g.O + f0) * g.HW;         // element index of (b, f0, 0)
@@ -194,16 +223,9 @@ __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uin
     const int fp = int(oddm & 2u);                   // first filter of the lane's pair stores
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-      uint32_t h[4];
-      finish(column(j), h);
       const int p = wr * RW * P + 16 * j + (lane & 15), row = p / P, col = p % P;
-      const uint32_t lo01 = h[0] | (h[1] << 16), lo23 = h[2] | (h[3] << 16);
-      const uint32_t send = (lo01 & oddm) | (lo23 & ~oddm);
-      const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap lane pairs
-      // even: (h0, recv.lo) and (h1, recv.hi); odd: (recv.lo, h2) and (recv.hi, h3)
-      const uint32_t wa_e = (h[0] & 0xffffu) | (recv << 16), wb_e = (h[1] & 0xffffu) | (recv & 0xffff0000u);
-      const uint32_t wa_o = (recv & 0xffffu) | (h[2] << 16), wb_o = (recv >> 16) | (h[3] << 16);
-      const uint32_t wa = (wa_o & oddm) | (wa_e & ~oddm), wb = (wb_o & oddm) | (wb_e & ~oddm);
+      uint32_t wa, wb;
+      round_pairs<E>(column(j), bv, g.relu, oddm, &wa, &wb);
       // the odd lane's pair starts at column c - 1, which is valid when its own column is
       const bool pv = col - int(oddm & 1u) < g.W && row < nrows;
       const int e = fbase + fp * g.HW + (oh0 + row) * g.W + col - int(oddm & 1u);
@@ -956,9 +978,236 @@ __global__ __launch_bounds__(256, 1) void slab_pipe_kernel(const uint16_t* __res
   slab_store<E, P, NBW, true>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
 }
 
+// ---- split form: loader waves beside the multiplying waves ----
+// The pipelined form's waves issue their own direct-to-LDS loads between MFMAs. Those loads are cheap in bandwidth
+// (the L2 serves the 36 KB a slice needs in a fraction of a step) but each one can hold its wave at issue while the
+// texture-address FIFO is full, and with one wave per SIMD the MFMA stream behind it waits too. This form gives
+// every SIMD a second wave that only loads: waves 0-3 multiply (their slot schedule has LDS reads, transposes and
+// MFMAs, no vector-memory instruction), waves 4-7 issue the same loads the pipelined form's waves 0-3 issue, wait for
+// them and meet the multiplying waves at the one barrier per step. The same LDS stages, load blocks and fragment
+// reads as the pipelined form.
+// Registers: two waves per SIMD leave each at most 256. The multiplying waves keep one set of weight fragments:
+// slice j's taps 5-8 are transposed at the start of step j (their last use in slice j - 1 was in step j - 1, their
+// first use in slice j comes after slot 35), then slice j + 1's weight runs are read over the same registers, and its
+// taps 0-4 are transposed at the end of step j, after their last use in slice j (slot 34).
+template <int P, int NBW>
+struct SplitSched {
+  static constexpr int G = P >= 16 ? 16 : P;
+  static constexpr int NBR = (16 * (NBW - 1) + 2 * P) / G + 1;
+  static constexpr int NM = 9 * NBW;
+  static constexpr int TL = 5;                   // taps 0 .. TL-1 transposed late, TL .. 8 early
+  static constexpr int NE = 4 * (9 - TL);        // early transposes (taps TL .. 8 of this step's slice)
+  static constexpr int NLATE = 4 * TL;           // late transposes (taps 0 .. TL-1 of the next slice)
+  static constexpr int NB = 2 * NBR;             // pixel-fragment reads of the next slice
+  static constexpr int E_END = NM * 2 / 7;       // early transposes within slots [0, E_END)
+  static constexpr int W_BEG = E_END;            // weight-run reads: slots W_BEG .. W_BEG + 8
+  static constexpr int B_BEG = W_BEG + 9;        // pixel reads after them
+  static constexpr int L_BEG = NM - (NLATE + 1) / 2 - 1;  // late transposes, two per slot, ending at the last slot
+  static constexpr int early_slot(int p) { return p * E_END / NE; }
+  static constexpr int wread_slot(int q) { return W_BEG + q; }
+  static constexpr int bread_slot(int q) { return B_BEG + q * (L_BEG - B_BEG) / NB; }
+  static constexpr int late_slot(int p) { return L_BEG + p / 2; }
+  static_assert(early_slot(NE - 1) < NBW * TL, "early transposes end before tap TL's first use (slot NBW * TL)");
+  static_assert(L_BEG >= NBW * TL, "late transposes start after the last use of tap TL - 1 (slot NBW * TL - 1)");
+  static_assert(B_BEG < L_BEG && late_slot(NLATE - 1) < NM, "slot plan");
+};
+
+template <typename E, int P, int NBW, int NST>
+__global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                           float* __restrict__ partial, SlabGeom g) {
+  using Sh = SlabShape<P, NBW, NST>;
+  using Sc = SplitSched<P, NBW>;
+  constexpr int CS = Sh::CS, NW = Sh::NW, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G, NBR = Sh::NBR;
+  constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
+  constexpr int ACT = Sh::ACT;
+  constexpr int WOFF = NST * ACT;      // LDS: [NST activation stages][NST weight stages]
+  constexpr int KA = ACT / 1024 / NW;  // 16-byte activation loads per loader per slice, two channel regions each
+  static_assert(CHP == 512 && KA * 2 == 8, "a loader's 8 channels take KA loads of two 512-byte channel regions");
+  constexpr int NI = KBW + KA;         // loads per loader per slice
+  constexpr int NM = Sc::NM, NB = Sc::NB, TL = Sc::TL;
+  constexpr int U = NST % 2 == 0 ? NST : 2 * NST;  // steps per loop turn: fragment set and stages are constants
+  static_assert(NST >= 3, "a slice loads NST - 1 steps ahead of its use");
+  static_assert((NST - 1) * NI < 64, "loads in flight fit the vmcnt counter");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+  args_in_sgprs(x, w, bias, y, partial, g);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slot = int(blockIdx.x);
+  const int unit = (slot >> 3) + (slot & 7) * g.per_xcd;
+  if (unit >= g.n_units) return;
+  const SlabUnit un = decode_unit(unit, g);
+  const int b = un.b, z = un.z;
+  const int o0 = un.ob * kSlTO, oh0 = un.band * RB;
+  int s_beg = 0, ns = g.S;
+  if (g.split > 1) {
+    s_beg = (g.S * z) / g.split;
+    ns = (g.S * (z + 1)) / g.split - s_beg;
+  }
+  const unsigned lds0 = lds_addr(lds);
+
+  if (wave >= NW) {
+    // ================= loader wave lw = wave - NW: the loads the pipelined form's wave lw issues =================
+    const int lw = wave - NW;
+    const v4i xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
+    const v4i x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: loads give zeros
+    int w_voff[KBW];
+    const int wrow = g.C * 18;  // bytes of one filter's OIHW weights
+#pragma unroll
+    for (int kb = 0; kb < KBW; ++kb) {
+      const int u = (lw + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
+      const int val = (o0 + f) * wrow + 16 * k;
+      const bool ok = (f < kSlTO) & (k < WCH) & (o0 + f < g.O);
+      w_voff[kb] = ok ? val : kOut;
+    }
+    int a_voff[2];
+    {
+      const int cl = lane >> 5, sslot = (lane >> 1) & 15, half = lane & 1;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int pos = ((sslot ^ seg_swz(8 * lw + 2 * e + cl)) << 4) + 8 * half;
+        const int row = pos / P, col = pos % P, ih = oh0 - 1 + row;
+        const int val = (cl * g.HW + ih * g.W + col) * 2;
+        const bool ok = (row < NR) & (unsigned(ih) < unsigned(g.H)) & (col < g.W);
+        a_voff[e] = ok ? val : kOut;
+      }
+    }
+    const int hw2 = g.HW * 2;
+    const int a_soff0 = (b * g.C + s_beg * CS + 8 * lw) * hw2;
+    const int w_soff0 = s_beg * CS * 18;
+    // load q of slice s into stage st: q < KA this loader's activation rows, then its weight blocks; slices past the
+    // unit's last load through zero-length resources (every step counts the same loads)
+    auto load_slice = [&](int s, int st) __attribute__((always_inline)) {
+      const bool real = s < ns;
+      const v4i xs = real ? xr : x0, ws = real ? wrs : w0;
+      const int a_soff = real ? a_soff0 + s * CS * hw2 : 0, w_soff = real ? w_soff0 + s * CS * 18 : 0;
+#pragma unroll
+      for (int q = 0; q < KA; ++q)
+        dma16s(xs, lds0 + unsigned(st * ACT + (lw * KA + q) * 1024), a_voff[q & 1], a_soff + 2 * q * hw2);
+#pragma unroll
+      for (int kb = 0; kb < KBW; ++kb)
+        dma16s(ws, lds0 + unsigned(WOFF + st * WST + (lw + NW * kb) * 1024), w_voff[kb], w_soff);
+    };
+    for (int s = 0; s < NST; ++s) load_slice(s, s);
+    wait_vmcnt<(NST - 1) * NI>();  // slice 0
+    stage_barrier();               // B0: slice 0 is in LDS
+    wait_vmcnt<(NST - 2) * NI>();  // slice 1
+    stage_barrier();               // start of step 0
+    for (int j = 0; j + 1 < ns; ++j) {
+      // step j: slice j was read in step j - 1, so its stage takes slice j + NST; slice j + 2 must land before the
+      // barrier that starts step j + 1
+      load_slice(j + NST, j % NST);
+      wait_vmcnt<(NST - 2) * NI>();
+      stage_barrier();
+    }
+    wait_vmcnt<0>();  // the zero loads past the last slice land before this wave ends
+    return;
+  }
+
+  // ================= multiplying wave: (filter half fh, row half wr) =================
+  const int fh = wave & 1, wr = wave >> 1;
+  const int nrows = min(RB, g.H - oh0);
+  const int f0 = o0 + fh * 16 + 4 * (lane >> 4);
+  uint32_t bbits[4];
+  {
+    const v4i br = make_vsharp(bias, g.split == 1 && bias != nullptr ? 2 * g.O : 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bbits[i] = load2s(br, 2 * min(f0 + i, g.O - 1), 0);
+  }
+  const unsigned a_rd = lds0 + unsigned(WOFF + (fh * 16 + (lane & 15)) * WPITCH + 8 * (lane >> 4) * 18);
+  unsigned b_rd[NBR][2];
+#pragma unroll
+  for (int u = 0; u < NBR; ++u) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ch = 8 * (lane >> 4) + 4 * h + ((lane & 15) >> 2);
+      const int pos = wr * RW * P + u * G + 4 * (lane & 3);
+      b_rd[u][h] = lds0 + unsigned(ch * CHP + (((pos >> 4) ^ seg_swz(ch)) << 5) + (pos & 15) * 2);
+    }
+  }
+  f32x4 acc[3][NBW];
+#pragma unroll
+  for (int s2 = 0; s2 < 3; ++s2) {
+#pragma unroll
+    for (int j2 = 0; j2 < NBW; ++j2) acc[s2][j2] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  u32x4 fw[9], fb[2][NBR];
+  uint32_t d[36];
+  auto read_w = [&](auto qc, auto st_c) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value, ST = decltype(st_c)::value;
+    const u32x4 v = rd16(a_rd + unsigned(ST * WST + 16 * q));
+    d[4 * q] = v.x, d[4 * q + 1] = v.y, d[4 * q + 2] = v.z, d[4 * q + 3] = v.w;
+  };
+  auto read_b = [&](auto qc, auto st_c, auto set_c) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value, ST = decltype(st_c)::value, S = decltype(set_c)::value;
+    constexpr int u = q / 2, h = q % 2;
+    const u32x2 v = rd_tr(b_rd[u][h] + unsigned(ST * ACT));
+    fb[S][u][2 * h] = v.x;
+    fb[S][u][2 * h + 1] = v.y;
+  };
+  // transpose p of tap t = p / 4: dword p % 4 of the tap's weight fragment (8 channels of one tap per lane)
+  auto perm_tap = [&](auto pc) __attribute__((always_inline)) {
+    constexpr int p = decltype(pc)::value, t = p / 4, c = p % 4;
+    fw[t][c] = pick2(d, 18 * c + t, 18 * c + 9 + t);
+  };
+  auto mfma_one = [&](auto kc, auto set_c) __attribute__((always_inline)) {
+    constexpr int k = decltype(kc)::value, S = decltype(set_c)::value;
+    constexpr int t = k / NBW, j = k % NBW, r = t / 3, sc = t % 3;
+    acc[sc][j] = E::mfma(fw[t], fb[S][(16 * j + r * P) / G], acc[sc][j]);
+  };
+
+  stage_barrier();  // B0: slice 0 is in LDS
+  // slice 0 into registers: its weight runs, its pixel fragments (set 0) and the transposes of taps 0 .. TL-1 (the
+  // others are done at the start of step 0, as in every step)
+  for_seq([&](auto qc) __attribute__((always_inline)) { read_w(qc, std::integral_constant<int, 0>{}); },
+          std::make_integer_sequence<int, 9>{});
+  for_seq([&](auto qc) __attribute__((always_inline)) {
+    read_b(qc, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+  }, std::make_integer_sequence<int, NB>{});
+  for_seq([&](auto pc) __attribute__((always_inline)) { perm_tap(pc); }, std::make_integer_sequence<int, 4 * TL>{});
+
+  // ---- step j (u = j mod U): slice j multiplies from pixel set u % 2 ----
+  auto step = [&](auto u_c) __attribute__((always_inline)) {
+    constexpr int uu = decltype(u_c)::value;
+    constexpr int cur = uu & 1, nxt = cur ^ 1, st_rd = (uu + 1) % NST;
+    stage_barrier();  // slice j + 1 has landed (the loaders waited), every wave is done with step j - 1
+    __builtin_amdgcn_sched_barrier(0);
+    for_seq([&](auto kc) __attribute__((always_inline)) {
+      constexpr int k = decltype(kc)::value;
+      mfma_one(kc, std::integral_constant<int, cur>{});
+      for_seq([&](auto pc) __attribute__((always_inline)) {
+        constexpr int p = decltype(pc)::value;
+        if constexpr (Sc::early_slot(p) == k) perm_tap(std::integral_constant<int, 4 * TL + p>{});
+      }, std::make_integer_sequence<int, Sc::NE>{});
+      for_seq([&](auto qc) __attribute__((always_inline)) {
+        if constexpr (Sc::wread_slot(decltype(qc)::value) == k) read_w(qc, std::integral_constant<int, st_rd>{});
+      }, std::make_integer_sequence<int, 9>{});
+      for_seq([&](auto qc) __attribute__((always_inline)) {
+        if constexpr (Sc::bread_slot(decltype(qc)::value) == k)
+          read_b(qc, std::integral_constant<int, st_rd>{}, std::integral_constant<int, nxt>{});
+      }, std::make_integer_sequence<int, NB>{});
+      for_seq([&](auto pc) __attribute__((always_inline)) {
+        if constexpr (Sc::late_slot(decltype(pc)::value) == k) perm_tap(pc);
+      }, std::make_integer_sequence<int, Sc::NLATE>{});
+      __builtin_amdgcn_sched_barrier(0);
+    }, std::make_integer_sequence<int, NM>{});
+  };
+  for (int j = 0; j < ns; j += U) {
+    for_seq([&](auto uc) __attribute__((always_inline)) {
+      if (j + decltype(uc)::value < ns) step(uc);
+    }, std::make_integer_sequence<int, U>{});
+  }
+  wait_vmcnt<0>();  // the bias loads
+#pragma unroll
+  for (int i = 0; i < 4; ++i) touch_v(bbits[i]);
+  slab_store<E, P, NBW, true>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
+}
+
 // kernel forms: slab_kernel (double-buffered fragments), slab_lean_kernel (single fragment set, at most 256
 // VGPR+AGPR), slab_pipe_kernel (double-buffered fragments, fixed slot schedule, whole slices)
-constexpr int kFull = 0, kLean = 1, kPipe = 2;
+constexpr int kFull = 0, kLean = 1, kPipe = 2, kSplit = 3;
 struct SlabCfg {
   int P, NBW, NST;
   int form;
@@ -967,7 +1216,7 @@ struct SlabCfg {
 constexpr SlabCfg kSlabCfgs[] = {{16, 7, 3, kFull}, {16, 7, 2, kFull}, {16, 4, 3, kFull}, {8, 2, 3, kFull},
                                  {8, 4, 3, kFull},  {32, 4, 3, kFull}, {16, 7, 2, kLean}, {16, 4, 2, kLean},
                                  {8, 2, 2, kLean},  {8, 4, 2, kLean},  {32, 4, 2, kLean}, {16, 7, 3, kLean},
-                                 {16, 7, 3, kPipe}};
+                                 {16, 7, 3, kPipe}, {16, 7, 3, kSplit}};
 constexpr int kSlabN = int(sizeof(kSlabCfgs) / sizeof(kSlabCfgs[0]));
 
 template <int I>
@@ -993,6 +1242,10 @@ SlabFn pick_fn(bool bf, int mode) {
     if (mode == kDma4)
       return bf ? &slab_pipe_kernel<Bf16, C::P, C::NBW, C::NST> : &slab_pipe_kernel<Fp16, C::P, C::NBW, C::NST>;
     return nullptr;
+  } else if constexpr (C::FORM == kSplit) {
+    if (mode == kDma4)
+      return bf ? &slab_split_kernel<Bf16, C::P, C::NBW, C::NST> : &slab_split_kernel<Fp16, C::P, C::NBW, C::NST>;
+    return nullptr;
   } else {
     if (mode == kDma4)
       return bf ? &slab_kernel<Bf16, C::P, C::NBW, C::NST, kDma4> : &slab_kernel<Fp16, C::P, C::NBW, C::NST, kDma4>;
@@ -1011,7 +1264,8 @@ struct SlabShapeInfo {
 template <int I>
 SlabShapeInfo shape_of() {
   using Sh = typename CfgT<I>::Sh;
-  return SlabShapeInfo{CfgT<I>::P, Sh::RB, Sh::CS, Sh::NT, CfgT<I>::LDS};
+  // the split form adds one loader wave per SIMD
+  return SlabShapeInfo{CfgT<I>::P, Sh::RB, Sh::CS, CfgT<I>::FORM == kSplit ? 2 * Sh::NT : Sh::NT, CfgT<I>::LDS};
 }
 
 template <int... Is>
@@ -1038,7 +1292,8 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   if (gg->batch <= 0 || gg->in_channels <= 0 || gg->out_channels <= 0 || gg->in_h <= 0 || gg->in_w <= 0)
     return GIE_HIP_EINVAL;
   if (gg->in_channels % 8 != 0) return GIE_HIP_EUNSUPPORTED;  // 16-byte chunks of the weight runs
-  if (kSlabCfgs[cfg].form == kPipe && gg->in_channels % 32 != 0) return GIE_HIP_EUNSUPPORTED;  // whole slices
+  if ((kSlabCfgs[cfg].form == kPipe || kSlabCfgs[cfg].form == kSplit) && gg->in_channels % 32 != 0)
+    return GIE_HIP_EUNSUPPORTED;  // whole slices
   const long long hw = 1LL * gg->in_h * gg->in_w;
   const bool bf = dtype == GIE_HIP_BF16;
   SlabShapeInfo si{};

@@ -113,8 +113,8 @@ struct Fns {
   static double extra_traffic(const ConvProblem& prob) {  // FP32 partials written and read back
     return e().split > 1 ? 2.0 * e().split * double(prob.p.output_shape().numel()) * 4.0 : 0.0;
   }
-  // the full and pipelined forms hold ~300-400 VGPR+AGPR per lane (one workgroup per CU); the lean form 256 at most
-  // (two)
+  // the full and pipelined forms hold ~300-400 VGPR+AGPR per lane (one workgroup per CU), the split form two waves
+  // per SIMD of at most 256 (one workgroup per CU); the lean form 256 at most (two workgroups)
   static int occupancy(const ConvProblem&) { return e().info.workgroups_per_cu; }
   // Useful output positions per step-equivalent: every slab of rows runs the step sequence of the widest
   // configuration (224 positions x 32 filters), whatever its own rows x pitch, because a step's time is set by its
@@ -196,7 +196,7 @@ void register_slab_family(std::vector<KernelDesc>& out) {
     k.name = std::string("slab_") + to_string(en.precision) + "_3x3_" + std::to_string(en.info.tile_m) + "x" +
              std::to_string(en.info.rows) + "r" + std::to_string(en.info.pitch) + "_k" +
              std::to_string(en.info.tile_k) + "_s" + std::to_string(en.info.stages) +
-             (en.info.form == 1 ? "_l" : en.info.form == 2 ? "_p" : "") +
+             (en.info.form == 1 ? "_l" : en.info.form == 2 ? "_p" : en.info.form == 3 ? "_ld" : "") +
              (en.info.workgroups_per_cu > 1 ? "_o" + std::to_string(en.info.workgroups_per_cu) : std::string()) + "_sk" +
              std::to_string(en.split);
     k.backend = Backend::kTensorCore;

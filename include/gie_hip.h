@@ -230,7 +230,8 @@ typedef struct gie_slab_config {
   int workgroups_per_cu; /* resident workgroups per CU: 2 for the lean form with at most 80 KiB LDS */
   int form;              /* 0: double-buffered fragments; 1: lean (single fragment set, at most 256 VGPR+AGPR);
                             2: pipelined (double-buffered fragments, one MFMA per issue slot carrying the side work;
-                            in_channels a multiple of 32) */
+                            in_channels a multiple of 32); 3: split (the pipelined layout with a second wave per
+                            SIMD that issues all loads, 512 threads; in_channels a multiple of 32) */
   int threads;
   int lds_bytes;
   int version;
