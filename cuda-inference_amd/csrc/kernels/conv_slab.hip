@@ -217,6 +217,42 @@ __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uin
       h[i] = E::from_f32(g.relu ? fmaxf(v, 0.0f) : v);
     }
   };
+  if constexpr (PADS_LOADED && P == 16) {
+    if (g.y_vec) {
+      // one 16-position block per output row: block j is row wr * RW + j, the lane's column is lane % 16. Pixel
+      // pairs as below, built with two packed conversions, two selects, one lane-pair swap and two byte permutes;
+      // the store offsets are a per-lane base (kOut for a column or filter outside the output) plus a wave-uniform
+      // row displacement, and rows past the slab's end are skipped by a uniform branch.
+      const uint32_t odd = uint32_t(lane & 1);
+      const int fp = int(odd) * 2, col = (lane & 15) - int(odd);
+      const uint32_t sel_a = odd ? 0x01000504u : 0x05040100u, sel_b = odd ? 0x03020706u : 0x07060302u;
+      const int row0 = oh0 + wr * RW;
+      const bool lane_ok = col < g.W && fp < nf;
+      const int base = lane_ok ? (fbase + fp * g.HW + row0 * g.W + col) * 2 : kOut;
+      const v4i yr = make_vsharp(y, int(g.total * 2));
+      auto rows = [&](auto relu_c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NBW; ++j) {
+          if (wr * RW + j >= nrows) break;
+          const f32x4 out = column(j);
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float t = out[i] + bv[i];
+            v[i] = decltype(relu_c)::value ? fmaxf(t, 0.0f) : t;
+          }
+          const uint32_t h01 = E::pack2(v[0], v[1]), h23 = E::pack2(v[2], v[3]);
+          const uint32_t send = odd ? h01 : h23, mine = odd ? h23 : h01;
+          const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap pairs
+          store4s(yr, base, 2 * j * g.W, __builtin_amdgcn_perm(recv, mine, sel_a));
+          store4s(yr, base, 2 * (j * g.W + g.HW), __builtin_amdgcn_perm(recv, mine, sel_b));
+        }
+      };
+      if (g.relu) rows(std::true_type{});
+      else rows(std::false_type{});
+      return;
+    }
+  }
   if (g.y_vec) {
     // pixel pairs: even lane (column c) stores filters 0, 1 at (c, c+1), odd lane filters 2, 3 at (c-1, c)
     const uint32_t oddm = 0u - uint32_t(lane & 1);  // all ones on odd lanes

@@ -36,6 +36,11 @@ struct Fp16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
                                                   0, 0);
   }
+  // two values rounded (nearest even) into one word, lo in bits 0-15: one v_cvt_pk_f16_f32 on gfx950
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, h2{(_Float16)lo, (_Float16)hi});
+  }
 };
 
 struct Bf16 {
@@ -54,6 +59,11 @@ struct Bf16 {
   static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
+  }
+  // two values rounded (nearest even, NaN quieted) into one word, lo in bits 0-15: one v_cvt_pk_bf16_f32 on gfx950
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, b2{(__bf16)lo, (__bf16)hi});
   }
 };
 

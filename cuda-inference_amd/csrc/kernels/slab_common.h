@@ -92,6 +92,13 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 __device__ __forceinline__ void store4(v4i rsrc, int voff, uint32_t v) {
   asm volatile("buffer_store_dword %0, %1, %2, 0 offen" ::"v"(v), "v"(voff), "s"(uniform4(rsrc)) : "memory");
 }
+// store4 with a wave-uniform byte offset added by the hardware (soffset): per-lane base offsets stay in registers
+// across a loop whose steps differ only by a uniform displacement
+__device__ __forceinline__ void store4s(v4i rsrc, int voff, int soff, uint32_t v) {
+  asm volatile("buffer_store_dword %0, %1, %2, %3 offen" ::"v"(v), "v"(voff), "s"(uniform4(rsrc)),
+               "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory");
+}
 __device__ __forceinline__ void store2(v4i rsrc, int voff, uint32_t v) {
   asm volatile("buffer_store_short %0, %1, %2, 0 offen" ::"v"(v), "v"(voff), "s"(uniform4(rsrc)) : "memory");
 }
