@@ -70,15 +70,7 @@ __device__ __forceinline__ void args_in_sgprs(const void* x, const void* w, cons
                "s"(g.sh_nz));
 }
 
-// 16 bytes into registers, not seen by the compiler as a load: valid after a counted wait (then touch_v)
-__device__ __forceinline__ u32x4 load16s(v4i rsrc, int voff, int soff) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
-               : "=v"(v)
-               : "v"(voff), "s"(uniform4(rsrc)), "s"(__builtin_amdgcn_readfirstlane(soff)));
-  return v;
-}
-__device__ __forceinline__ void wr16(unsigned a, u32x4 v) { *reinterpret_cast<lds_v4*>(size_t(a)) = v; }
+
 
 template <int P, int NBW, int KH>
 struct StackShape {

@@ -58,6 +58,7 @@ constexpr FamilyProfile kFamilies[] = {
     {"stem_", 0.25, 0.555, 2.0},     // L4 30.9 us = 3.95 TB/s
     {"narrow_", 0.084, 0.30, 2.0},  // L5 15.0 us (123 TFLOP/s)
     {"stack_", 0.33, 0.40, 4.1},    // L5 10.0 us at split 2 (7.0 conv + reduce), 10.2 at split 1, 10.5 at split 4
+    {"deep_", 0.40, 0.40, 3.0},     // L5: one launch, whole reduction per workgroup
     {"f32_", 0.30, 0.35, 2.0},      // FP32 / TF32 vector kernels: not benchmarked, assumed
 };
 

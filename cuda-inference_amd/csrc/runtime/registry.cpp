@@ -20,6 +20,7 @@ void register_stem_family(std::vector<KernelDesc>& out);  // stem_family.cpp
 void register_narrow_family(std::vector<KernelDesc>& out);  // narrow_family.cpp
 void register_slab_family(std::vector<KernelDesc>& out);    // slab_family.cpp
 void register_stack_family(std::vector<KernelDesc>& out);   // stack_family.cpp
+void register_deep_family(std::vector<KernelDesc>& out);    // deep_family.cpp
 
 std::string KernelDesc::describe() const {
   std::ostringstream os;
@@ -43,6 +44,7 @@ std::vector<KernelDesc>& registry_storage() {
     register_narrow_family(r);  // likewise
     register_slab_family(r);    // likewise
     register_stack_family(r);   // likewise
+    register_deep_family(r);    // likewise
     std::set<std::string> names;
     for (const auto& k : r) {
       if (!names.insert(k.name).second) throw Error(StatusCode::kInternal, "duplicate kernel name " + k.name);

@@ -217,6 +217,8 @@ _HIP = {
     "gie_hip_conv_slab": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_conv_slab_noalloc": ([_i, _i, _GP, _vp, _vp, _vp, _vp, _i, _vp], _i),
     "gie_hip_slab_scratch_floats": ([], ctypes.c_longlong),
+    "gie_hip_deep_check": ([_GP, _ip], _i),
+    "gie_hip_conv_deep": ([_i, _GP, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_stack_config_count": ([], _i),
     "gie_hip_stack_config_get": ([_i, ctypes.POINTER(GieStackConfig)], _i),
     "gie_hip_stack_check": ([_i, _GP, _ip, _ip], _i),

@@ -30,6 +30,8 @@
  *                                    layers, fused: one launch straight from NCHW x / OIHW w
  *                                                                         src/kernels/tensor_core_mma.cu:61-82,99-251,297-324
  *   gie_hip_slab_config_*            the registered tile table             src/kernels/tensor_core_mma.cu:370-388
+ *   gie_hip_conv_deep, _deep_check   both transposes + tcmma_kernel + splitk_reduce for 3x3 stride-1 layers over
+ *                                    small images with long reductions, fused into one launch without split-K
  *   gie_hip_conv_stack, _stack_check both transposes + tcmma_kernel (split-K partials included) for 3x3 stride-1
  *                                    layers with small images and a long reduction, fused: one launch straight from
  *                                    NCHW x / OIHW w, images of a group stacked in one plane
@@ -291,6 +293,17 @@ int gie_hip_stack_check(int config, const gie_conv_geom* g, int* lds_bytes, int*
    floor(S*(z+1)/split)), S = in_channels / 32; reduce with gie_hip_splitk_reduce. 1 <= split <= S. */
 int gie_hip_conv_stack(int config, int dtype, const gie_conv_geom* g, const void* x, const void* w,
                        const void* bias, void* y, float* partial, int split, void* stream);
+
+/* Deep-reduction convolution on MFMA 16x16x32 (FP32 accumulation) straight from the caller's NCHW x and OIHW w, for
+   3x3 stride-1 padding-1 layers over small images (in_h <= 8, in_w <= 7) with in_channels % 128 == 0: one workgroup
+   per (16-filter block, image) sums the whole reduction (four waves over interleaved channel slices, partial tiles
+   added in LDS in a fixed order), so there is no split-K and no workspace. y (NCHW) = round(relu?(acc + bias)), one
+   rounding. x 4-byte aligned and w 16-byte aligned (GIE_HIP_EUNSUPPORTED otherwise); y and bias 2-byte aligned.
+   Replaces, for these shapes, the tcmma launch sequence of src/kernels/tensor_core_mma.cu:297-324 (two transposes,
+   tcmma_kernel, splitk_reduce). *_check: 0 when the geometry runs, with the LDS bytes per workgroup. */
+int gie_hip_deep_check(const gie_conv_geom* g, int* lds_bytes);
+int gie_hip_conv_deep(int dtype, const gie_conv_geom* g, const void* x, const void* w, const void* bias, void* y,
+                      void* stream);
 
 /* y[i] = round(relu?(sum_{z=0..split-1, ascending} partial[z*total+i] + bias[(i / hw_out) % out_channels]));
    dtype GIE_HIP_FP32 / _TF32: y and bias are float and there is no rounding step. */

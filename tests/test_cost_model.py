@@ -19,7 +19,7 @@ BENCH = {
     "c2_fp16_3x3": (P(32, 256, 14, 14, 256, 3, 3, 1, 1, 1, 1, precision="fp16", has_bias=True, relu=True), "slab_"),
     "c3_fp16_1x1": (P(64, 256, 28, 28, 1024, 1, 1, 1, 1, 0, 0, precision="fp16", has_bias=True, relu=True), "pw_"),
     "c4_fp16_7x7s2": (P(64, 3, 224, 224, 64, 7, 7, 2, 2, 3, 3, precision="fp16", has_bias=True, relu=True), "stem_"),
-    "c5_bf16_3x3": (P(8, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, precision="bf16", has_bias=True, relu=True), "stack_"),
+    "c5_bf16_3x3": (P(8, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, precision="bf16", has_bias=True, relu=True), "deep_"),
 }
 
 
