@@ -65,19 +65,10 @@ def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
     opts = dict(kernel=kernel) if kernel else dict(autotune=True, cache_path=tune_cache)
     kernel, source, _ = gie.select(p, **opts)
     ws = gie.DeviceBuffer(gie.workspace_size(p, **opts))
-    # correctness of the exact call being timed, against the library's GPU double reference
-    gie.forward(p, t, ws, stream, **opts)
-    stream.sync()
-    y = t.y().astype(np.float64)
-    ref, _ = gie.gpu_reference(p, t)
-    ref = ref.astype(np.float64)
-    if p.precision == "bf16":
-        ref_r = (gie.storage_to_float(gie.host_to_storage(ref.astype(np.float32), "bf16"), "bf16")).astype(np.float64)
-    else:
-        ref_r = ref
-    rel_l2 = float(np.linalg.norm(y - ref_r) / np.linalg.norm(ref_r))
-    max_abs = float(np.abs(y - ref).max())
-    # timed region: exactly `steps` forward calls between two events on the stream
+    # timed region: `warmup` untimed calls, then exactly `steps` forward calls between two events on the stream.
+    # The output of the last timed call is what the correctness check below reads; the check (an FP64 reference
+    # convolution on the GPU plus host-side comparison) runs after the timing so it does not sit in front of it.
+    t.poison()
     gie.forward_n(p, t, ws, stream, warmup, **opts)
     stream.sync()
     e0, e1 = gie.Event(), gie.Event()
@@ -91,6 +82,16 @@ def run_config(gie, name, cfg, steps, warmup, stream, tune_cache, kernel=None):
     us_call = ms * 1e3 / steps
     flops = p.flops()
     tflops = flops / (us_call * 1e-6) / 1e12
+    # correctness of the timed calls' output, against the library's GPU double reference
+    y = t.y().astype(np.float64)
+    ref, _ = gie.gpu_reference(p, t)
+    ref = ref.astype(np.float64)
+    if p.precision == "bf16":
+        ref_r = (gie.storage_to_float(gie.host_to_storage(ref.astype(np.float32), "bf16"), "bf16")).astype(np.float64)
+    else:
+        ref_r = ref
+    rel_l2 = float(np.linalg.norm(y - ref_r) / np.linalg.norm(ref_r))
+    max_abs = float(np.abs(y - ref).max())
     # the reference harness's protocol (benchmark_main.cpp:55-56, timing.cpp:42-83): warm-up 5, then 30 samples of
     # back-to-back forward calls lasting >= 1 ms each, median per call
     med = gie.time_forward(p, t, ws, stream, warmup=5, samples=30, min_sample_ms=1.0, **opts)
@@ -285,6 +286,12 @@ def dominant_kernel(registry_name: str) -> str:
     """The device function that does the multiply-accumulate work for a registry kernel (the rocprof kernel name)."""
     if registry_name.startswith("slab_") and "_l_" in registry_name:
         return "slab_lean_kernel (3x3 MFMA convolution straight from NCHW / OIHW, lean form, conv_slab.hip)"
+    if registry_name.startswith("slab_") and "_ld_" in registry_name:
+        return ("slab_split_kernel (3x3 MFMA convolution straight from NCHW / OIHW, split form: loader waves beside "
+                "the multiplying waves, conv_slab.hip)")
+    if registry_name.startswith("deep_"):
+        return ("deep_kernel (3x3 MFMA convolution of small images, whole reduction per workgroup, loader waves, "
+                "conv_deep.hip)")
     if registry_name.startswith("slab_") and "_p_" in registry_name:
         return "slab_pipe_kernel (3x3 MFMA convolution straight from NCHW / OIHW, pipelined form, conv_slab.hip)"
     stems = [("slab_", "slab_kernel (3x3 MFMA convolution straight from NCHW / OIHW, conv_slab.hip)"),
@@ -332,6 +339,8 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        ap.error("--steps must be >= 1 and --warmup >= 0")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the Conv2D library is a "
               "single-GPU operator; across GPUs each rank would run its own share of the batch with the same "
@@ -360,9 +369,9 @@ def main():
     head = None
     for name in names:
         log(f"[bench] {name}: tuning + timing")
-        steps = args.steps if name == HEADLINE else max(100, args.steps // 4)
-        p, t, r = run_config(gie, name, CONFIGS[name], steps, args.warmup if name == HEADLINE else 50, stream,
-                             args.tune_cache, args.kernel if name == HEADLINE else None)
+        # every config under the same protocol: --warmup untimed calls, then exactly --steps timed calls
+        p, t, r = run_config(gie, name, CONFIGS[name], args.steps, args.warmup, stream, args.tune_cache,
+                             args.kernel if name == HEADLINE else None)
         log(f"[bench] {name}: {r['kernel']} {r['us_per_call']:.2f} us/call {r['tflops']:.1f} TFLOP/s "
             f"(median protocol {r['median_protocol']['us_per_call']:.2f} us; gemm {r['stage_us']['gemm_us']:.2f} us, "
             f"repack {r['stage_us']['repack_us']:.2f} us) rel_l2={r['rel_l2']:.2e}")
@@ -375,8 +384,7 @@ def main():
         best = fastest_split_entry(gie, CONFIGS[SPLITK], stream)
         if best:
             log(f"[bench] {SPLITK}: forced split-K entry {best}")
-            _, _, r = run_config(gie, SPLITK, CONFIGS[SPLITK], max(100, args.steps // 4), 50, stream,
-                                 args.tune_cache, best)
+            _, _, r = run_config(gie, SPLITK, CONFIGS[SPLITK], args.steps, args.warmup, stream, args.tune_cache, best)
             r["selection"] = "forced: fastest split_k > 1 entry by a short plan timing"
             log(f"[bench] {SPLITK} split-K: {r['kernel']} {r['us_per_call']:.2f} us/call, reduce "
                 f"{r['stage_us']['reduce_us']:.2f} us = {r['reduce_gbs'] or 0:.0f} GB/s")
