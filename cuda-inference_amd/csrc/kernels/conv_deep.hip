@@ -65,8 +65,37 @@ struct DeepGeom {
   int relu;
   int total;            // |Y| elements
   int items;            // activation (channel, row) items per step: 128 * H
+  unsigned h_magic;     // e / H = (e * h_magic) >> 16 for e < 1024 (h_magic = ceil(2^16 / H))
   unsigned keep[4];     // dword masks keeping a row's W columns
 };
+
+// (e * ceil(2^16 / H)) >> 16 == e / H for every H in 1 .. 8 and e < 1024: the product exceeds e * 2^16 / H by at most
+// e (H - 1) / H < 1024 * 7 / 8, which stays below 2^16 / H, the distance from e / H to the next integer.
+constexpr bool deep_magic_exact() {
+  for (unsigned h = 1; h <= 8; ++h)
+    for (unsigned e = 0; e < 1024; ++e)
+      if (((e * ((65536u + h - 1) / h)) >> 16) != e / h) return false;
+  return true;
+}
+static_assert(deep_magic_exact(), "division by in_h through a multiplier");
+
+// The weight chunk c of a step (c < 2560) splits into slice q = c / 592 and r = c % 592, and r into filter
+// f = r / 37 and piece k = r % 37, through multipliers: the products stay below 2^24, so they are 24-bit multiplies.
+constexpr bool deep_chunk_magic_exact() {
+  for (unsigned c = 0; c < 2560; ++c)
+    if (((c * 7085u) >> 22) != c / 592) return false;
+  for (unsigned r = 0; r < 592; ++r)
+    if (((r * 1772u) >> 16) != r / 37) return false;
+  return true;
+}
+static_assert(deep_chunk_magic_exact(), "chunk decomposition through multipliers");
+static_assert(kDpRun == 37 * 16 && kDpWq == 592 * 16 && kDpKW * 256 <= 2560, "chunk decomposition constants");
+
+// v if ok, else the out-of-range offset, with bit operations (a conditional would become an exec-mask branch)
+__device__ __forceinline__ unsigned deep_sel(bool ok, unsigned v) {
+  const unsigned m = 0u - unsigned(ok);
+  return (v & m) | (unsigned(kOut) & ~m);
+}
 
 __device__ __forceinline__ int deep_tau(int ch) { return (ch & 3) | (((ch >> 3) & 1) << 2); }
 // byte offset of (channel plane, plane row) inside an activation stage; ch is the channel's index in the stage (the
@@ -124,26 +153,35 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
     const int lw = wave - 4, lt = tid - 256;
     const v4i xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
     const v4i x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: zeros, no traffic
-    // zero the plane rows no load writes (row 0 and rows in_h + 1 .. 9) of both stages, once
-    const int zr = kDpRows - g.H;  // zero rows per channel
-    for (int i = lt; i < 2 * kDpQ * kDpCS * zr; i += 256) {
-      const int st = i / (kDpQ * kDpCS * zr), rem = i - st * (kDpQ * kDpCS * zr);
-      const int ch = rem / zr, z = rem - ch * zr;
-      wr16(lds0 + unsigned(st * kDpAct + deep_granule(ch, z == 0 ? 0 : g.H + z)), u32x4{0u, 0u, 0u, 0u});
-    }
-    // weight chunk c of a step: slice q, filter f, 16-byte piece k of the run (k = 36 is the pad)
+    // weight chunk c = (4 kb + lw) * 64 + lane of a step: slice q, filter f, 16-byte piece k of the run (k = 36 is
+    // the pad, never read)
     int w_voff[kDpKW];
-    const int wrow = g.C * 18;
+    const unsigned wrow = unsigned(g.C) * 18u;  // < 2^24 (deep_prepare)
+    const unsigned cb = unsigned(lw * 64 + lane);
 #pragma unroll
     for (int kb = 0; kb < kDpKW; ++kb) {
-      const int c = (kb * 4 + lw) * 64 + lane, q = c / (kDpTO * 37), r = c - q * kDpTO * 37;
-      const int f = r / 37, k = r - f * 37;
-      const bool ok = (c < kDpWch) & (k < 36) & (o0 + f < g.O);
-      w_voff[kb] = ok ? (o0 + f) * wrow + q * 576 + 16 * k : kOut;
+      const unsigned c = cb + 256u * unsigned(kb);
+      const unsigned q = __umul24(c, 7085u) >> 22, r = c - __umul24(q, 592u);
+      const unsigned f = __umul24(r, 1772u) >> 16, k = r - __umul24(f, 37u);
+      const bool ok = (c < unsigned(kDpWch)) & (k < 36u) & (o0 + int(f) < g.O);
+      w_voff[kb] = int(deep_sel(ok, __umul24(unsigned(o0) + f, wrow) + __umul24(q, 576u) + 16u * k));
     }
+    const int a_step = kDpQ * kDpCS * g.HW * 2, w_step = kDpQ * 576;
+    // step t's weights into stage st by DMA
+    auto load_w = [&](int t, int st) __attribute__((always_inline)) {
+      const bool real = t < g.NS;
+      const v4i ws = real ? wrs : w0;
+      const int ws_off = real ? t * w_step : 0;
+#pragma unroll
+      for (int kb = 0; kb < kDpKW; ++kb)
+        dma16s(ws, lds0 + unsigned(kDpWOff + st * kDpWst + (kb * 4 + lw) * 1024), w_voff[kb], ws_off);
+    };
+    load_w(0, 0);  // the first loads leave before any other set-up work
+    __builtin_amdgcn_sched_barrier(0);
     // activation item e = k * 256 + lt: (channel ch of the step's 128, row r); the row's W halves start at element
     // (b * C + ch) * HW + r * W; the load starts at the 4-byte boundary at or below it
     constexpr int KA = (kDpQ * kDpCS * 8 + 255) / 256;  // up to 8 rows per channel
+    const int x_img = b * g.C * g.HW;                    // first element of the image (uniform)
     int a_voff[KA];
     uint32_t a_sh[KA];
     unsigned a_dst[KA];
@@ -153,24 +191,24 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
       const int e = k * 256 + lt;
       a_ok[k] = e < g.items;
       const int ee = a_ok[k] ? e : 0;
-      const int ch = ee / g.H, r = ee - ch * g.H;
-      const int elem = (b * g.C + ch) * g.HW + r * g.W;
+      const int ch = int(__umul24(unsigned(ee), g.h_magic) >> 16), r = ee - ch * g.H;
+      const int elem = x_img + int(__umul24(unsigned(ch), unsigned(g.HW)) + __umul24(unsigned(r), unsigned(g.W)));
       a_voff[k] = a_ok[k] ? ((elem * 2) & ~3) : kOut;
       a_sh[k] = uint32_t(elem & 1) << 4;
       a_dst[k] = lds0 + unsigned(deep_granule(ch, r + 1));
     }
-    const int a_step = kDpQ * kDpCS * g.HW * 2, w_step = kDpQ * 576;
     u32x4 ra[KA], rb[KA];
-    // step t's loads: weights into stage st by DMA, activation rows into registers (the caller writes them)
-    auto load_step = [&](int t, int st, u32x4 (&rr)[KA]) __attribute__((always_inline)) {
+    // step t's activation rows into registers (write_rows puts them in LDS)
+    auto load_a = [&](int t, u32x4 (&rr)[KA]) __attribute__((always_inline)) {
       const bool real = t < g.NS;
-      const v4i xs = real ? xr : x0, ws = real ? wrs : w0;
-      const int as = real ? t * a_step : 0, ws_off = real ? t * w_step : 0;
-#pragma unroll
-      for (int kb = 0; kb < kDpKW; ++kb)
-        dma16s(ws, lds0 + unsigned(kDpWOff + st * kDpWst + (kb * 4 + lw) * 1024), w_voff[kb], ws_off);
+      const v4i xs = real ? xr : x0;
+      const int as = real ? t * a_step : 0;
 #pragma unroll
       for (int k = 0; k < KA; ++k) rr[k] = load16s(xs, a_voff[k], as);
+    };
+    auto load_step = [&](int t, int st, u32x4 (&rr)[KA]) __attribute__((always_inline)) {
+      load_w(t, st);
+      load_a(t, rr);
     };
     auto write_rows = [&](int st, u32x4 (&rr)[KA]) __attribute__((always_inline)) {
 #pragma unroll
@@ -185,8 +223,16 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
         if (a_ok[k]) wr16(a_dst[k] + unsigned(st * kDpAct), o);
       }
     };
-    load_step(0, 0, ra);
+    load_a(0, ra);
     load_step(1, 1, rb);
+    // zero the plane rows no load writes (row 0 and rows in_h + 1 .. 9) of both stages, once: loader thread lt
+    // takes channel lt % 128 of stage lt / 128
+    {
+      const unsigned zbase = lds0 + unsigned((lt >> 7) * kDpAct);
+      const int zch = lt & 127;
+      for (int z = 0; z < kDpRows - g.H; ++z)
+        wr16(zbase + unsigned(deep_granule(zch, z == 0 ? 0 : g.H + z)), u32x4{0u, 0u, 0u, 0u});
+    }
     wait_vmcnt<kDpKW + KA>();  // step 0's loads (step 1's may be in flight)
     write_rows(0, ra);
     stage_barrier();  // B0: step 0 in LDS
@@ -337,6 +383,7 @@ int deep_prepare(const gie_conv_geom* gg, DeepGeom* g) {
   const long long xb = 2LL * gg->batch * gg->in_channels * hw, wb = 18LL * gg->out_channels * gg->in_channels;
   const long long total = 1LL * gg->batch * gg->out_channels * hw;
   if (xb >= (1LL << 30) || wb >= (1LL << 30) || total >= (1LL << 29)) return GIE_HIP_EUNSUPPORTED;
+  if (18LL * gg->in_channels >= (1LL << 24)) return GIE_HIP_EUNSUPPORTED;  // a filter's OIHW row: 24-bit multiplies
   const long long units = 1LL * gg->batch * ((gg->out_channels + kDpTO - 1) / kDpTO);
   if (units > (1LL << 24)) return GIE_HIP_EUNSUPPORTED;
   g->B = gg->batch, g->C = gg->in_channels, g->H = gg->in_h, g->W = gg->in_w, g->O = gg->out_channels;
@@ -348,6 +395,7 @@ int deep_prepare(const gie_conv_geom* gg, DeepGeom* g) {
   g->relu = gg->relu;
   g->total = int(total);
   g->items = kDpQ * kDpCS * gg->in_h;
+  g->h_magic = (65536u + unsigned(gg->in_h) - 1) / unsigned(gg->in_h);
   for (int i = 0; i < 4; ++i) {
     const int lo = 2 * i, hi = 2 * i + 1;  // columns of dword i
     g->keep[i] = (lo < gg->in_w ? 0xffffu : 0u) | (hi < gg->in_w ? 0xffff0000u : 0u);
