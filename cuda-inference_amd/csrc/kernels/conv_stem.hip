@@ -202,14 +202,13 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   for (int fh = 0; fh < 2; ++fh)
 #pragma unroll
     for (int s = 0; s < KS; ++s) wa[fh][s] = frag[((fh * 32 + col) * KS + s) * 2 + hi];
-  // per-lane byte offset of the row each k-step reads, from the lane's (output row 0, column 0) position (the bias
-  // and zero groups read group 0: any valid address, replaced below)
-  int offs[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const int grp = 2 * s + hi < NG ? 2 * s + hi : 0;
-    offs[s] = ((grp / 7) * WR + grp % 7) * g.RS * 4;
-  }
+  // Row each k-step reads, from the lane's (output row 0, column 0) position: group 2s's row r0(s) (a constant per
+  // step, times the row stride: uniform), plus for the hi half (group 2s + 1) one row further, or WR - 6 rows (the
+  // next channel's first filter row) when group 2s is a channel's last filter row. The bias and zero groups read
+  // group 2s's row or group 0's (any valid address: replaced below). Two per-lane displacements instead of one
+  // offset register per step.
+  const int rs4 = g.RS * 4;
+  const int h_next = hi * rs4, h_chan = hi * (WR - 6) * rs4;
   stage_barrier();  // tile 0's rows are in
 
   // ---- multiplying waves: 32-pixel blocks of tile i from row buffer i % 3, in pairs (wave, wave + 7), (wave + 14,
@@ -252,7 +251,10 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
       const unsigned char* bp = rb + (2 * r * g.RS + ow + 2) * 4;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const uint32_t* q = reinterpret_cast<const uint32_t*>(bp + offs[s]);
+        const int g0 = 2 * s;
+        const int r0 = g0 < NG ? (g0 / 7) * WR + g0 % 7 : 0;
+        const int dl = g0 + 1 < NG ? (g0 % 7 == 6 ? h_chan : h_next) : 0;
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(bp + r0 * rs4 + dl);
         d[s][0] = q[0], d[s][1] = q[1], d[s][2] = q[2], d[s][3] = q[3];
       }
     };
@@ -322,8 +324,9 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   }
 }
 
-// Geometry of a stem launch; GIE_HIP_EUNSUPPORTED when the problem is not one this kernel runs.
-int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
+// Geometry of a stem launch; GIE_HIP_EUNSUPPORTED when the problem is not one this kernel runs. max_r caps the
+// output rows per tile (4, or 2 for a variant whose 4-row form does not fit the register file).
+int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds, int max_r = 4) {
   if (!gg) return GIE_HIP_EINVAL;
   if (gg->kernel_h != 7 || gg->kernel_w != 7 || gg->stride_h != 2 || gg->stride_w != 2 || gg->pad_h != 3 ||
       gg->pad_w != 3)
@@ -343,7 +346,7 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
   g->rows_off = (64 * g->C * 49 * 2 + 15) / 16 * 16 + 64 * ks * 2 * 16 + 128;  // weights, operands, bias
   int R = 0;
   for (int r : {4, 2})
-    if (g->rows_off + kStBufs * g->C * (2 * r + 5) * g->RS * 4 + kStCW * 4096 <= kStLdsMax) {
+    if (r <= max_r && g->rows_off + kStBufs * g->C * (2 * r + 5) * g->RS * 4 + kStCW * 4096 <= kStLdsMax) {
       R = r;
       break;
     }
@@ -366,13 +369,20 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds) {
 
 using StemFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, StemGeom);
 
+// BF16 with four channels and ReLU runs 2-row tiles: its 4-row form needs more than the 256 registers a wave has at
+// two waves per SIMD, and a spill would add scratch traffic to the vector-memory counter the row-streaming wave
+// counts. That form is never instantiated.
+constexpr bool stem_two_rows_only(bool bf16, int c, bool relu) { return bf16 && c == 4 && relu; }
+
 template <typename E, int R, bool RELU>
 StemFn stem_fn(int c) {
   switch (c) {
     case 1: return &stem_kernel<E, 1, R, RELU>;
     case 2: return &stem_kernel<E, 2, R, RELU>;
     case 3: return &stem_kernel<E, 3, R, RELU>;
-    default: return &stem_kernel<E, 4, R, RELU>;
+    default:
+      if constexpr (R == 4 && stem_two_rows_only(E::kDtype == GIE_HIP_BF16, 4, RELU)) return nullptr;
+      else return &stem_kernel<E, 4, R, RELU>;
   }
 }
 
@@ -399,13 +409,15 @@ extern "C" int gie_hip_conv_stem(int dtype, const gie_conv_geom* gg, const void*
   if (bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) return GIE_HIP_EINVAL;
   StemGeom g;
   int lds = 0;
-  if (int rc = stem_prepare(gg, current_device_cus(), &g, &lds)) return rc;
+  const bool bf = dtype == GIE_HIP_BF16;
+  const int max_r = stem_two_rows_only(bf, gg->in_channels, gg->relu != 0) ? 2 : 4;
+  if (int rc = stem_prepare(gg, current_device_cus(), &g, &lds, max_r)) return rc;
   // 16-byte input row and weight loads, 16-byte output stores
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
       (reinterpret_cast<uintptr_t>(y) & 15u))
     return GIE_HIP_EUNSUPPORTED;
-  const bool bf = dtype == GIE_HIP_BF16;
   const StemFn fn = bf ? stem_fn<Bf16>(g.C, g.R, gg->relu != 0) : stem_fn<Fp16>(g.C, g.R, gg->relu != 0);
+  if (fn == nullptr) return GIE_HIP_EUNSUPPORTED;
   if (int rc = set_lds_limit(reinterpret_cast<const void*>(fn), lds)) return rc;
   const unsigned grid = unsigned(g.G * ((g.O + 63) / 64));
   hipLaunchKernelGGL(fn, dim3(grid), dim3(kStNT), lds, static_cast<hipStream_t>(stream),
