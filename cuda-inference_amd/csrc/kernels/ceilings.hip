@@ -28,6 +28,9 @@ __global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src
 }
 
 __global__ void empty_kernel() {}
+__global__ void empty_kernel_ptr(int* sink) {
+  if (threadIdx.x == 4096 && sink) sink[0] = 0;
+}
 
 __global__ __launch_bounds__(256) void fill_u16_kernel(uint16_t* __restrict__ dst, long long n, uint16_t v) {
   for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -65,6 +68,29 @@ extern "C" int gie_hip_ceiling_copy(const void* src, void* dst, size_t bytes, vo
 
 extern "C" int gie_hip_ceiling_empty(void* stream) {
   hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream));
+  return launched();
+}
+
+namespace {
+// an argument block of N dwords that the kernel reads (one lane of a lane id no launch has), so nothing is dropped
+template <int N>
+struct ArgBlock {
+  int v[N];
+};
+template <int N>
+__global__ void empty_args_kernel(ArgBlock<N> a, int* sink) {
+  if (threadIdx.x == 4096 && sink) sink[0] = a.v[N - 1];
+}
+}  // namespace
+
+extern "C" int gie_hip_ceiling_empty_args(int arg_bytes, void* stream) {
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (arg_bytes) {
+    case 8: hipLaunchKernelGGL(empty_kernel_ptr, dim3(1), dim3(64), 0, s, static_cast<int*>(nullptr)); break;
+    case 128: hipLaunchKernelGGL(empty_args_kernel<30>, dim3(1), dim3(64), 0, s, ArgBlock<30>{}, nullptr); break;
+    case 1024: hipLaunchKernelGGL(empty_args_kernel<254>, dim3(1), dim3(64), 0, s, ArgBlock<254>{}, nullptr); break;
+    default: return GIE_HIP_EINVAL;
+  }
   return launched();
 }
 

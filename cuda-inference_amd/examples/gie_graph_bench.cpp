@@ -13,7 +13,8 @@
 //   * Three experiments, each a function returning records: chain (graph vs eager per depth, with a bitwise check of
 //     repeated replays against the eager chain), fanout (S independent layers on one stream vs one stream each, joined
 //     back), and floor (graphs of N empty kernels launched as instantiated, and again after hipGraphUpload, against N
-//     eager empty launches) — the floor separates what a graph launch costs from what the layers cost.
+//     eager empty launches) — the floor separates what a graph launch costs from what the layers cost — and launch
+//     arguments (one eager empty launch with 0, 8, 128 and 1024 argument bytes).
 //   * Output: one JSON record per measurement appended to <out>/graphs.jsonl; with --md FILE the same results as
 //     markdown tables.
 //
@@ -23,6 +24,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
@@ -317,6 +319,31 @@ std::vector<json::Value> floor_experiment(const Probe& probe, const DeviceInfo& 
   return out;
 }
 
+// What one eager launch costs the host as a function of its argument block: the empty kernel with 0, 8, 128 and
+// 1024 argument bytes, host time per enqueue (batches alternating with the 0-byte launch) and device time per launch
+// back to back. The record carries HIP_FORCE_DEV_KERNARG as set for the run (HIP's default copies a non-empty block
+// to device memory).
+std::vector<json::Value> launch_args_experiment(const Probe& probe, const DeviceInfo& dev) {
+  std::vector<json::Value> out;
+  const char* env = std::getenv("HIP_FORCE_DEV_KERNARG");
+  const Enqueue none = [](hipStream_t s) { check_kernel_status(gie_hip_ceiling_empty(s), "empty kernel"); };
+  for (const int bytes : {0, 8, 128, 1024}) {
+    const Enqueue with_args = [bytes](hipStream_t s) {
+      if (bytes == 0) check_kernel_status(gie_hip_ceiling_empty(s), "empty kernel");
+      else check_kernel_status(gie_hip_ceiling_empty_args(bytes, s), "empty kernel with arguments");
+    };
+    const auto [host_none, host_args] = probe.host_us(none, with_args);
+    json::Value r = record("F_launch_args", dev);
+    r["arg_bytes"] = bytes;
+    r["HIP_FORCE_DEV_KERNARG"] = env ? std::string(env) : std::string("unset");
+    r["host_launch_us"] = host_args;
+    r["host_launch_us_no_args"] = host_none;
+    r["device_us"] = probe.device_us(with_args);
+    out.push_back(r);
+  }
+  return out;
+}
+
 // ---- reporting ---------------------------------------------------------------------------------------------------------
 
 std::string fmt(double v, int digits = 1) {
@@ -343,6 +370,15 @@ std::string markdown(const std::vector<json::Value>& rows) {
          << fmt(num(*r, "eager_host_launch_us")) << " → " << fmt(num(*r, "graph_host_launch_us")) << " → "
          << fmt(num(*r, "uploaded_graph_host_launch_us")) << " | " << fmt(num(*r, "eager_device_us")) << " → "
          << fmt(num(*r, "graph_device_us")) << " → " << fmt(num(*r, "uploaded_graph_device_us")) << " |\n";
+    md << "\n";
+  }
+  if (const auto a = of("F_launch_args"); !a.empty()) {
+    md << "| argument bytes | HIP_FORCE_DEV_KERNARG | host µs per launch (0-byte launch alongside) | device µs per "
+          "launch |\n|---|---|---|---|\n";
+    for (const json::Value* r : a)
+      md << "| " << num(*r, "arg_bytes") << " | " << str(*r, "HIP_FORCE_DEV_KERNARG") << " | "
+         << fmt(num(*r, "host_launch_us"), 2) << " (" << fmt(num(*r, "host_launch_us_no_args"), 2) << ") | "
+         << fmt(num(*r, "device_us"), 2) << " |\n";
     md << "\n";
   }
   if (const auto c = of("F_hip_graphs"); !c.empty()) {
@@ -429,7 +465,10 @@ int main(int argc, char** argv) {
         jsonl.flush();
         std::cout.flush();
       };
-      if (args.floor) emit(floor_experiment(probe, dev));
+      if (args.floor) {
+        emit(launch_args_experiment(probe, dev));
+        emit(floor_experiment(probe, dev));
+      }
       for (int ci = 0; ci < args.cases; ++ci) {
         const ConvProblem prob = problem_of(kLayerCases[ci], args.precision);
         const KernelDesc& kernel = kernel_for(prob, dev, args.kernel);

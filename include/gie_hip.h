@@ -334,6 +334,10 @@ int gie_hip_reference_conv(int dtype, const gie_conv_geom* g, const void* x, con
 int gie_hip_ceiling_mfma(int blocks, int iters, float* sink, void* stream);
 int gie_hip_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream);
 int gie_hip_ceiling_empty(void* stream);
+/* The empty kernel with an argument block of arg_bytes (8: one pointer; 128; 1024): what a launch costs the host as a
+   function of its kernel arguments (HIP copies a non-empty block to device memory by default). GIE_HIP_EINVAL for
+   other sizes. No counterpart in the reference: a measurement of this build's launch path. */
+int gie_hip_ceiling_empty_args(int arg_bytes, void* stream);
 
 /* dst[i] = value for i < n (16-bit elements, any 2-byte alignment). A graph-safe fill (no memset node). */
 int gie_hip_fill_u16(void* dst, int64_t n, uint16_t value, void* stream);
