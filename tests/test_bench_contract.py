@@ -23,6 +23,9 @@ def test_more_than_one_gpu_is_refused_with_a_message():
 @pytest.mark.parametrize("name,fn", [
     ("slab_fp16_3x3_32x14r16_k32_s2_l_o2_sk1", "slab_lean_kernel"),
     ("slab_fp16_3x3_32x14r16_k32_s3_p_sk1", "slab_pipe_kernel"),
+    ("slab_fp16_3x3_32x14r16_k32_s3_ld_sk1", "slab_split_kernel"),
+    ("deep_bf16_3x3_16x8r8_k32x4_ld", "deep_kernel"),
+    ("stack_bf16_3x3_32x8r8_k32_sk2", "stack_kernel"),
     ("slab_bf16_3x3_32x8r8_k32_s3_sk2", "slab_kernel"),
     ("band_fp16_3x3_32x224x32_s4_sk1", "band_kernel"),
     ("halo_bf16_3x3_64x128x32_s2_sk4", "halo_kernel"),

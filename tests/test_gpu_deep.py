@@ -104,3 +104,12 @@ def test_deep_argument_checks():
                                                                 precision="fp16")):
         gb = bad.geom(bad.in_channels)
         assert h.gie_hip_deep_check(ctypes.byref(gb), None) == -2
+
+
+def test_dispatcher_routes_config5_to_the_deep_entry():
+    """The cost model alone (no tuning) picks the deep entry, measured fastest for BASELINE config 5."""
+    c = dict(BENCH_CONFIGS["c5_bf16_3x3_splitk"])
+    prec = c.pop("precision")
+    p = gie.Problem(**c, precision=prec, has_bias=True, relu=True)
+    k, src, _ = gie.select(p)
+    assert k == "deep_bf16_3x3_16x8r8_k32x4_ld" and src == "cost_model", (k, src)

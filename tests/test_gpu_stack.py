@@ -137,15 +137,6 @@ def test_stack_argument_checks():
     assert h.gie_hip_conv_stack(99, 1, ctypes.byref(g), d.addr, d.addr, None, d.addr, None, 1, None) == -1
 
 
-def test_dispatcher_routes_config5_to_the_stack_family():
-    """The cost model alone (no tuning) picks the stack entry measured fastest for BASELINE config 5 (split 2)."""
-    c = dict(BENCH_CONFIGS["c5_bf16_3x3_splitk"])
-    prec = c.pop("precision")
-    p = gie.Problem(**c, precision=prec, has_bias=True, relu=True)
-    k, src, _ = gie.select(p)
-    assert k == "stack_bf16_3x3_32x8r8_k32_sk2" and src == "cost_model", (k, src)
-
-
 def test_stack_repeated_launches_agree_bitwise():
     """Regression: register loads issued for the slices past the last one once landed in registers the epilogue had
     reused, corrupting a few outputs when the loads were slow (two workgroups sharing a CU, or real data behind
