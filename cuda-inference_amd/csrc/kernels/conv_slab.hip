@@ -1126,11 +1126,16 @@ __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __re
       for (int kb = 0; kb < KBW; ++kb)
         dma16s(ws, lds0 + unsigned(WOFF + st * WST + (lw + NW * kb) * 1024), w_voff[kb], w_soff);
     };
-    for (int s = 0; s < NST; ++s) load_slice(s, s);
-    wait_vmcnt<(NST - 1) * NI>();  // slice 0
-    stage_barrier();               // B0: slice 0 is in LDS
-    wait_vmcnt<(NST - 2) * NI>();  // slice 1
-    stage_barrier();               // start of step 0
+    // slices 0 and 1 first, so the first slice shares the cold start's bandwidth with one other slice, not two;
+    // slice 2 goes out once slice 0 has landed
+    static_assert(NST == 3, "the start-up sequence below issues slices 0, 1 and then 2");
+    load_slice(0, 0);
+    load_slice(1, 1);
+    wait_vmcnt<NI>();  // slice 0
+    stage_barrier();   // B0: slice 0 is in LDS
+    load_slice(2, 2);
+    wait_vmcnt<NI>();  // slice 1
+    stage_barrier();   // start of step 0
     for (int j = 0; j + 1 < ns; ++j) {
       // step j: slice j was read in step j - 1, so its stage takes slice j + NST; slice j + 2 must land before the
       // barrier that starts step j + 1
