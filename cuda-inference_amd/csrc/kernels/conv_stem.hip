@@ -47,7 +47,7 @@ struct StemGeom {
   int CPR;        // 16-byte chunks per input row (in_w / 8 <= 64)
   int RS;         // LDS row stride in dwords: in_w / 2 + 8
   int buf_bytes;  // one row buffer: C * WR * RS * 4
-  int rows_off;   // LDS byte offset of the row buffers (after the prologue's weights)
+  int rows_off;   // LDS byte offset of the row buffers (after the MFMA operands)
   int tile_off;   // LDS byte offset of the multiplying waves' output tiles (4 KiB each)
   int x_bytes, y_bytes;
 };
@@ -140,42 +140,44 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
     reinterpret_cast<uint32_t*>(smem + g.rows_off)[rw * g.RS + dw] = 0u;
   }
 
-  // ---- the workgroup's 64 filters: raw OIHW block (16-byte aligned: 64 * C * 49 halves per group) and the bias
-  // into LDS, then the MFMA operands
-  uint16_t* wl = reinterpret_cast<uint16_t*>(smem);
-  constexpr int kWBytes = (64 * FW * 2 + 15) / 16 * 16;
-  constexpr int kFragBytes = 64 * KS * 2 * 16;
-  u32x4* frag = reinterpret_cast<u32x4*>(smem + kWBytes);
-  uint16_t* bl = reinterpret_cast<uint16_t*>(smem + kWBytes + kFragBytes);
+  // ---- the MFMA operands of the workgroup's 64 filters, built straight from OIHW: operand (filter f, k-step s,
+  // half h) is group grp = 2s + h, the 7 taps of one filter row (channel grp / 7, row grp % 7), which are 7
+  // consecutive halves of the filter's OIHW run starting at element 7 grp. One 16-byte load from the 4-byte boundary
+  // at or below them, a 16-bit shift when they start at an odd element, and byte permutes put them in the order
+  // kw 0, 2, 4, 6, 1, 3, 5, 0. The bias group holds (bias, 0, ...); groups past it are zero. Stored [f][s][h] x 16
+  // bytes at the start of LDS.
+  u32x4* frag = reinterpret_cast<u32x4*>(smem);
   if (wave != kStLoader) {  // (the streaming wave keeps its vector-memory counter to the row loads)
-    constexpr int kMT = kStCW * 64;                               // threads of the multiplying waves
-    constexpr int kW16 = (64 * FW * 2 / 16 + kMT - 1) / kMT;      // 16-byte chunks per thread
-    const int nh = nf * FW, n16 = nh >> 3;
-    const u32x4* w16 = reinterpret_cast<const u32x4*>(w + size_t(f0) * FW);
-    u32x4 tmp[kW16];
+    constexpr int kMT = kStCW * 64;                         // threads of the multiplying waves
+    constexpr int kItems = 64 * KS * 2;                     // operands
+    constexpr int kPer = (kItems + kMT - 1) / kMT;          // operands per thread
+    const v4i wrs = make_vsharp(w, g.O * FW * 2);           // dwords past w read as zeros
+    u32x4 v[kPer];
+    uint32_t sh[kPer], bv[kPer];
 #pragma unroll
-    for (int k = 0; k < kW16; ++k) tmp[k] = w16[min(tid + k * kMT, n16 - 1)];  // all loads in flight at once
-    if (tid < nh - n16 * 8) wl[n16 * 8 + tid] = w[size_t(f0) * FW + n16 * 8 + tid];
-    if (tid < nf) bl[tid] = bias != nullptr ? bias[f0 + tid] : uint16_t(0);
-#pragma unroll
-    for (int k = 0; k < kW16; ++k)
-      if (tid + k * kMT < n16) *reinterpret_cast<u32x4*>(wl + (tid + k * kMT) * 8) = tmp[k];
-  }
-  __syncthreads();
-  // operand (filter f, k-step s, half h) = 8 halves of group 2s + h: kw 0, 2, 4, 6, 1, 3, 5, 0; the bias group
-  // holds (bias, 0, ...); groups past it are zero. Stored [f][s][h] x 16 bytes.
-  for (int idx = tid; idx < 64 * KS * 2; idx += kStNT) {
-    const int f = idx / (2 * KS), grp = idx - f * 2 * KS;  // grp = 2s + h
-    uint32_t h[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (f < nf) {
-      if (grp < NG) {
-        const uint16_t* p = wl + f * FW + (grp / 7) * 49 + (grp % 7) * 7;
-        h[0] = p[0], h[1] = p[2], h[2] = p[4], h[3] = p[6], h[4] = p[1], h[5] = p[3], h[6] = p[5];
-      } else if (grp == NG) {
-        h[0] = bl[f];
-      }
+    for (int k = 0; k < kPer; ++k) {  // every load in flight before the first is used
+      const int idx = tid + k * kMT, f = idx / (2 * KS), grp = idx - f * 2 * KS;
+      const bool real = idx < kItems && f < nf;
+      const int e = (f0 + f) * FW + 7 * grp;
+      v[k] = load16_asm(wrs, real && grp < NG ? (2 * e) & ~3 : kOut);
+      sh[k] = uint32_t(e & 1) << 4;
+      bv[k] = real && grp == NG && bias != nullptr ? uint32_t(bias[f0 + f]) : 0u;
     }
-    frag[idx] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    wait_vm<0>();
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int idx = tid + k * kMT, f = idx / (2 * KS), grp = idx - f * 2 * KS;
+      if (idx >= kItems) break;
+      touch_v(v[k]);
+      const u32x4 d = v[k];
+      const uint32_t q0 = __builtin_amdgcn_alignbit(d.y, d.x, sh[k]), q1 = __builtin_amdgcn_alignbit(d.z, d.y, sh[k]);
+      const uint32_t q2 = __builtin_amdgcn_alignbit(d.w, d.z, sh[k]), q3 = __builtin_amdgcn_alignbit(0u, d.w, sh[k]);
+      // q0..q3 = halves (p0, p1), (p2, p3), (p4, p5), (p6, -): the operand is (p0, p2), (p4, p6), (p1, p3), (p5, 0)
+      u32x4 op = {__builtin_amdgcn_perm(q1, q0, 0x05040100u), __builtin_amdgcn_perm(q3, q2, 0x05040100u),
+                  __builtin_amdgcn_perm(q1, q0, 0x07060302u), q2 >> 16};
+      if (grp >= NG || f >= nf) op = u32x4{bv[k], 0u, 0u, 0u};  // the bias group, or zero
+      frag[idx] = op;
+    }
   }
   __syncthreads();
 
@@ -343,7 +345,7 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds, int ma
   g->CPR = g->W / 8;
   g->RS = g->W / 2 + 2 * kStPad;
   const int ks = (7 * g->C + 2) / 2;
-  g->rows_off = (64 * g->C * 49 * 2 + 15) / 16 * 16 + 64 * ks * 2 * 16 + 128;  // weights, operands, bias
+  g->rows_off = 64 * ks * 2 * 16;  // the MFMA operands
   int R = 0;
   for (int r : {4, 2})
     if (r <= max_r && g->rows_off + kStBufs * g->C * (2 * r + 5) * g->RS * 4 + kStCW * 4096 <= kStLdsMax) {

@@ -30,7 +30,9 @@ CASES = [
     (3, 2, 17, 32, 70, "fp16", True, True),       # C = 2, odd output height, two filter groups
     (2, 4, 40, 48, 128, "bf16", False, True),     # C = 4, no bias
     (1, 3, 9, 16, 64, "fp16", True, True),        # smallest width: out_w 8, three tiles only
-    (1, 4, 6, 336, 64, "fp16", True, True),       # widest rows that fit LDS with C = 4 (336 columns)
+    (1, 4, 6, 304, 64, "fp16", True, True),       # widest C = 4 rows with 4-row tiles in LDS (304 columns)
+    (1, 4, 6, 464, 64, "fp16", True, True),       # widest C = 4 rows that fit LDS (464 columns, 2-row tiles)
+    (2, 4, 9, 464, 64, "bf16", True, True),       # the same in BF16 with ReLU (2-row tiles always)
     (1, 3, 4, 512, 64, "bf16", True, True),       # widest rows (512 columns)
     (4, 3, 64, 64, 32, "bf16", True, True),       # filter count 32
     (2, 3, 30, 48, 64, "fp16", False, False),     # no epilogue
@@ -66,7 +68,7 @@ def test_stem_geometry_and_argument_checks():
                 gie.Problem(2, 3, 32, 32, 64, 7, 7, 2, 2, 2, 2, precision="fp16"),   # padding 2
                 _problem(2, 5, 32, 32, 64, "fp16", True, True),                     # C = 5
                 _problem(2, 3, 32, 40, 64, "fp16", True, True),                     # in_w % 16 != 0
-                _problem(1, 4, 6, 352, 64, "fp16", True, True),                     # rows too wide for LDS
+                _problem(1, 4, 6, 480, 64, "fp16", True, True),                     # rows too wide for LDS
                 _problem(1, 3, 6, 528, 64, "fp16", True, True)):                    # rows over 512 columns
         assert h.gie_hip_stem_check(ctypes.byref(bad.geom(bad.in_channels)), None) != 0
     ok = _problem(2, 3, 32, 32, 64, "fp16", True, True)
