@@ -135,7 +135,8 @@ def test_stem_geometry_check_on_host():
     """gie_hip_stem_check is host arithmetic: every shape the GPU stem tests launch qualifies within the LDS limit,
     and the geometries the kernel cannot run are refused."""
     ok = [(2, 3, 32, 32, 64), (1, 1, 16, 16, 20), (3, 2, 17, 32, 70), (2, 4, 40, 48, 128), (1, 3, 9, 16, 64),
-          (1, 4, 6, 336, 64), (1, 3, 4, 512, 64), (4, 3, 64, 64, 32), (2, 3, 30, 48, 64), (64, 3, 224, 224, 64)]
+          (1, 4, 6, 304, 64), (1, 4, 6, 464, 64), (2, 4, 9, 464, 64), (1, 3, 4, 512, 64), (4, 3, 64, 64, 32),
+          (2, 3, 30, 48, 64), (64, 3, 224, 224, 64)]
     for B, C, H, W, K in ok:
         p = gie.Problem(B, C, H, W, K, 7, 7, 2, 2, 3, 3, precision="fp16")
         lds = ctypes.c_int(0)
@@ -145,7 +146,7 @@ def test_stem_geometry_check_on_host():
               gie.Problem(2, 3, 32, 32, 64, 7, 7, 1, 1, 3, 3, precision="fp16"),
               gie.Problem(2, 5, 32, 32, 64, 7, 7, 2, 2, 3, 3, precision="fp16"),
               gie.Problem(2, 3, 32, 40, 64, 7, 7, 2, 2, 3, 3, precision="fp16"),
-              gie.Problem(1, 4, 6, 352, 64, 7, 7, 2, 2, 3, 3, precision="fp16"),
+              gie.Problem(1, 4, 6, 480, 64, 7, 7, 2, 2, 3, 3, precision="fp16"),
               gie.Problem(1, 3, 6, 528, 64, 7, 7, 2, 2, 3, 3, precision="fp16")):
         assert gie.hip().gie_hip_stem_check(ctypes.byref(p.geom(p.in_channels)), None) != 0
 
