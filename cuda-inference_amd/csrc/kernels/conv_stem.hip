@@ -4,18 +4,18 @@
 // The generic implicit GEMM pads C to 8 channels per tap (K = 49 * 8 = 392 for C = 3); the stem's reduction is
 // only C * 49 = 147 long and the layer is bound by writing Y (64 filters per pixel), so this kernel keeps the
 // reduction short and spends its effort on the stores.
-//   * K order: one group of 8 per (channel c, filter row kh): the even filter columns kw = 0, 2, 4, 6, then the
-//     odd ones kw = 1, 3, 5, then a zero. With stride 2 the 7 input pixels of one (c, kh) group are the input
-//     columns 2*ow - 3 .. 2*ow + 3, inside the 4 dwords of the row that start at column 2*ow - 4; reordered that
-//     way, the group's 16-byte operand is formed from those 4 dwords with 4 bit operations. 7*C groups plus one
-//     bias group (weights = bias, pixels = 1.0 at its first k), in k-steps of two groups: K = 176 for C = 3
-//     (147 useful).
+//   * K order: one group of 8 per (channel c, filter row kh): a zero, then the filter columns kw = 0 .. 6. With
+//     stride 2 the 7 input pixels of one (c, kh) group are the input columns 2*ow - 3 .. 2*ow + 3, so k = kw + 1
+//     meets column 2*ow - 4 + k: the group's 16-byte pixel operand is the 4 dwords of the row that start at column
+//     2*ow - 4 as they lie in LDS, with their first half (column 2*ow - 4, weight zero) cleared by one AND so that
+//     an Inf or NaN outside the window cannot reach the sum. 7*C groups plus one bias group (weights = bias, pixels
+//     = 1.0 at its first k), in k-steps of two groups: K = 176 for C = 3 (147 useful).
 //   * A workgroup (one per CU, persistent) owns 64 filters and walks tiles of R = 4 (2 for wide rows) output rows of
 //     one image (R * out_w pixels, contiguous in each output plane). The tile's 2R+5 input rows per channel sit in LDS with 4 zero
 //     dwords on each side (the horizontal padding); rows above or below the image are loaded as zeros. Wave 7
 //     streams rows: tile i+2's rows go straight into the third of three row buffers (buffer_load ... lds) while
 //     waves 0..6 multiply tile i. Waves 0..6 hold the 64 filters' operands in registers (2 x 32 columns x K);
-//     per 32-pixel block: two ds_read2_b32 and 4 bit operations per k-step, two MFMA chains. One barrier per tile.
+//     per 32-pixel block: two ds_read2_b32 and one AND per k-step, two MFMA chains. One barrier per tile.
 //   * MFMA roles: rows = pixels, columns = filters, so each lane's accumulators hold 4-pixel runs of one filter.
 //     Epilogue: ReLU, RNE rounding (the order of the reference's apply_epilogue,
 //     src/kernels/fused_epilogue.cuh:11-16), the wave's 64-filter x 32-pixel tile staged in LDS, 16-byte stores
@@ -143,9 +143,9 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   // ---- the MFMA operands of the workgroup's 64 filters, built straight from OIHW: operand (filter f, k-step s,
   // half h) is group grp = 2s + h, the 7 taps of one filter row (channel grp / 7, row grp % 7), which are 7
   // consecutive halves of the filter's OIHW run starting at element 7 grp. One 16-byte load from the 4-byte boundary
-  // at or below them, a 16-bit shift when they start at an odd element, and byte permutes put them in the order
-  // kw 0, 2, 4, 6, 1, 3, 5, 0. The bias group holds (bias, 0, ...); groups past it are zero. Stored [f][s][h] x 16
-  // bytes at the start of LDS.
+  // at or below them and 16-bit shifts put them in the order (0, kw 0, ..., kw 6): k = kw + 1 meets input column
+  // 2 ow - 4 + k, so the pixel operand is the row's 16 bytes from column 2 ow - 4 as they lie in LDS. The bias group
+  // holds (bias, 0, ...); groups past it are zero. Stored [f][s][h] x 16 bytes at the start of LDS.
   u32x4* frag = reinterpret_cast<u32x4*>(smem);
   if (wave != kStLoader) {  // (the streaming wave keeps its vector-memory counter to the row loads)
     constexpr int kMT = kStCW * 64;                         // threads of the multiplying waves
@@ -172,9 +172,9 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
       const u32x4 d = v[k];
       const uint32_t q0 = __builtin_amdgcn_alignbit(d.y, d.x, sh[k]), q1 = __builtin_amdgcn_alignbit(d.z, d.y, sh[k]);
       const uint32_t q2 = __builtin_amdgcn_alignbit(d.w, d.z, sh[k]), q3 = __builtin_amdgcn_alignbit(0u, d.w, sh[k]);
-      // q0..q3 = halves (p0, p1), (p2, p3), (p4, p5), (p6, -): the operand is (p0, p2), (p4, p6), (p1, p3), (p5, 0)
-      u32x4 op = {__builtin_amdgcn_perm(q1, q0, 0x05040100u), __builtin_amdgcn_perm(q3, q2, 0x05040100u),
-                  __builtin_amdgcn_perm(q1, q0, 0x07060302u), q2 >> 16};
+      // q0..q3 = halves (p0, p1), (p2, p3), (p4, p5), (p6, -): the operand is (0, p0), (p1, p2), (p3, p4), (p5, p6)
+      u32x4 op = {q0 << 16, __builtin_amdgcn_alignbit(q1, q0, 16), __builtin_amdgcn_alignbit(q2, q1, 16),
+                  __builtin_amdgcn_alignbit(q3, q2, 16)};
       if (grp >= NG || f >= nf) op = u32x4{bv[k], 0u, 0u, 0u};  // the bias group, or zero
       frag[idx] = op;
     }
@@ -264,13 +264,9 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
       acc0 = f32x16{0}, acc1 = f32x16{0};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        // halves h0..h7 = input columns 2*ow-4 .. 2*ow+3; the group is (h1, h3, h5, h7, h2, h4, h6, 0): one byte
-        // permute per dword (bytes 0-3 of the second operand, 4-7 of the first)
-        u32x4 b;
-        b.x = __builtin_amdgcn_perm(d[s][1], d[s][0], 0x07060302u);  // kw 0, 2: high halves of dwords 0 and 1
-        b.y = __builtin_amdgcn_perm(d[s][3], d[s][2], 0x07060302u);  // kw 4, 6
-        b.z = __builtin_amdgcn_perm(d[s][2], d[s][1], 0x05040100u);  // kw 1, 3: low halves of dwords 1 and 2
-        b.w = d[s][3] & 0xffffu;                                      // kw 5, 0
+        // halves h0..h7 = input columns 2*ow-4 .. 2*ow+3 meet weights (0, kw 0, ..., kw 6): the operand is the
+        // window as read, h0 zeroed (its weight is zero, but an Inf or NaN there would still reach the sum)
+        u32x4 b = {d[s][0] & 0xffff0000u, d[s][1], d[s][2], d[s][3]};
         const int grp = 2 * s + hi;
         if (2 * s + 1 >= NG) {  // this step holds the bias group (and possibly the zero group)
           if (grp == NG) b = u32x4{one_bits<E>(), 0u, 0u, 0u};
