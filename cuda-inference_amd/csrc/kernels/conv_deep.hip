@@ -132,6 +132,33 @@ static_assert(DeepSched::late_slot(0) >= kDpNB * DeepSched::TL, "late transposes
 static_assert(DeepSched::bread_slot(17) < DeepSched::NM && DeepSched::late_slot(4 * DeepSched::TL - 1) < DeepSched::NM,
               "slot plan");
 
+// Offsets of the weight chunks share lw (0..3) of a step issues: chunk c = (4 kb + lw) * 64 + lane is slice q,
+// filter f, 16-byte piece k of the run (k = 36 is the pad, never read); out-of-range chunks get kOut.
+__device__ __forceinline__ void deep_w_offsets(int lw, int lane, int o0, const DeepGeom& g, int (&w_voff)[kDpKW]) {
+  const unsigned wrow = unsigned(g.C) * 18u;  // < 2^24 (deep_prepare)
+  const unsigned cb = unsigned(lw * 64 + lane);
+#pragma unroll
+  for (int kb = 0; kb < kDpKW; ++kb) {
+    const unsigned c = cb + 256u * unsigned(kb);
+    const unsigned q = __umul24(c, 7085u) >> 22, r = c - __umul24(q, 592u);
+    const unsigned f = __umul24(r, 1772u) >> 16, k = r - __umul24(f, 37u);
+    const bool ok = (c < unsigned(kDpWch)) & (k < 36u) & (o0 + int(f) < g.O);
+    w_voff[kb] = int(deep_sel(ok, __umul24(unsigned(o0) + f, wrow) + __umul24(q, 576u) + 16u * k));
+  }
+}
+
+// Step t's share lw of the weights into stage st by direct-to-LDS loads (kDpKW of them; past the last step they go
+// through a zero-length resource).
+__device__ __forceinline__ void deep_load_w(const uint16_t* w, const DeepGeom& g, unsigned lds0, int lw,
+                                            const int (&w_voff)[kDpKW], int t, int st) {
+  const bool real = t < g.NS;
+  const v4i ws = make_vsharp(w, real ? g.w_bytes : 0);
+  const int ws_off = real ? t * kDpQ * 576 : 0;
+#pragma unroll
+  for (int kb = 0; kb < kDpKW; ++kb)
+    dma16s(ws, lds0 + unsigned(kDpWOff + st * kDpWst + (kb * 4 + lw) * 1024), w_voff[kb], ws_off);
+}
+
 template <typename E>
 __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ w,
@@ -153,29 +180,10 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
     const int lw = wave - 4, lt = tid - 256;
     const v4i xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
     const v4i x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: zeros, no traffic
-    // weight chunk c = (4 kb + lw) * 64 + lane of a step: slice q, filter f, 16-byte piece k of the run (k = 36 is
-    // the pad, never read)
     int w_voff[kDpKW];
-    const unsigned wrow = unsigned(g.C) * 18u;  // < 2^24 (deep_prepare)
-    const unsigned cb = unsigned(lw * 64 + lane);
-#pragma unroll
-    for (int kb = 0; kb < kDpKW; ++kb) {
-      const unsigned c = cb + 256u * unsigned(kb);
-      const unsigned q = __umul24(c, 7085u) >> 22, r = c - __umul24(q, 592u);
-      const unsigned f = __umul24(r, 1772u) >> 16, k = r - __umul24(f, 37u);
-      const bool ok = (c < unsigned(kDpWch)) & (k < 36u) & (o0 + int(f) < g.O);
-      w_voff[kb] = int(deep_sel(ok, __umul24(unsigned(o0) + f, wrow) + __umul24(q, 576u) + 16u * k));
-    }
-    const int a_step = kDpQ * kDpCS * g.HW * 2, w_step = kDpQ * 576;
-    // step t's weights into stage st by DMA
-    auto load_w = [&](int t, int st) __attribute__((always_inline)) {
-      const bool real = t < g.NS;
-      const v4i ws = real ? wrs : w0;
-      const int ws_off = real ? t * w_step : 0;
-#pragma unroll
-      for (int kb = 0; kb < kDpKW; ++kb)
-        dma16s(ws, lds0 + unsigned(kDpWOff + st * kDpWst + (kb * 4 + lw) * 1024), w_voff[kb], ws_off);
-    };
+    deep_w_offsets(lw, lane, o0, g, w_voff);
+    const int a_step = kDpQ * kDpCS * g.HW * 2;
+    auto load_w = [&](int t, int st) __attribute__((always_inline)) { deep_load_w(w, g, lds0, lw, w_voff, t, st); };
     load_w(0, 0);  // the first loads leave before any other set-up work
     __builtin_amdgcn_sched_barrier(0);
     // activation item e = k * 256 + lt: (channel ch of the step's 128, row r); the row's W halves start at element
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
       }
     };
     load_a(0, ra);
-    load_step(1, 1, rb);
+    load_a(1, rb);  // step 1's weights: the multiplying waves issue them (eight waves load the first two stages)
     // zero the plane rows no load writes (row 0 and rows in_h + 1 .. 9) of both stages, once: loader thread lt
     // takes channel lt % 128 of stage lt / 128
     {
@@ -233,7 +241,7 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
       for (int z = 0; z < kDpRows - g.H; ++z)
         wr16(zbase + unsigned(deep_granule(zch, z == 0 ? 0 : g.H + z)), u32x4{0u, 0u, 0u, 0u});
     }
-    wait_vmcnt<kDpKW + KA>();  // step 0's loads (step 1's may be in flight)
+    wait_vmcnt<KA>();  // step 0's loads (step 1's activation rows may be in flight)
     write_rows(0, ra);
     stage_barrier();  // B0: step 0 in LDS
     wait_vmcnt<0>();
@@ -253,6 +261,13 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
   }
 
   // ====================== multiplying wave w: slices 4t + w ======================
+  // First, step 1's weight share w (the loaders issue every other load of the first two stages): more waves issuing
+  // load instructions move the cold start's bytes from L2 faster
+  {
+    int w_voff[kDpKW];
+    deep_w_offsets(wave, lane, o0, g, w_voff);
+    deep_load_w(w, g, lds0, wave, w_voff, 1, 1);
+  }
   using Sc = DeepSched;
   constexpr int NM = Sc::NM, TL = Sc::TL;
   const int wv = wave;
@@ -337,6 +352,7 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
       __builtin_amdgcn_sched_barrier(0);
     }, std::make_integer_sequence<int, NM>{});
   };
+  wait_vmcnt<4>();  // this wave's share of step 1's weights (the 4 bias loads after them may be in flight)
   for (int t = 0; t < g.NS; t += 2) {
     step(I0{});
     if (t + 1 < g.NS) step(std::integral_constant<int, 1>{});
