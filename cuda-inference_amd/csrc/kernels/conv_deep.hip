@@ -49,6 +49,7 @@ constexpr int kDpRun = 576 + 16;              // weight run of one filter and sl
 constexpr int kDpWq = kDpTO * kDpRun;         // one slice's weights
 constexpr int kDpWch = kDpQ * kDpWq / 16;     // 16-byte chunks of a step's weights (37 per run)
 constexpr int kDpKW = (kDpWch + 255) / 256;   // weight loads per loader lane and step (10)
+constexpr int kDpKWh = kDpKW / 2;             // from step 2 on, a loader issues the first kDpKWh, its partner the rest
 constexpr int kDpWst = kDpKW * 4 * 1024;      // weight stage: every load block of the four loaders (40 KiB)
 constexpr int kDpWOff = 2 * kDpAct;
 constexpr int kDpXOff = kDpWOff + 2 * kDpWst;  // partial-tile exchange: 4 waves x 4 blocks x 64 lanes x 16 bytes
@@ -147,15 +148,16 @@ __device__ __forceinline__ void deep_w_offsets(int lw, int lane, int o0, const D
   }
 }
 
-// Step t's share lw of the weights into stage st by direct-to-LDS loads (kDpKW of them; past the last step they go
-// through a zero-length resource).
+// Step t's share lw of the weights into stage st by direct-to-LDS loads: load blocks KB0 .. KB1-1 of the share (past
+// the last step they go through a zero-length resource).
+template <int KB0 = 0, int KB1 = kDpKW>
 __device__ __forceinline__ void deep_load_w(const uint16_t* w, const DeepGeom& g, unsigned lds0, int lw,
                                             const int (&w_voff)[kDpKW], int t, int st) {
   const bool real = t < g.NS;
   const v4i ws = make_vsharp(w, real ? g.w_bytes : 0);
   const int ws_off = real ? t * kDpQ * 576 : 0;
 #pragma unroll
-  for (int kb = 0; kb < kDpKW; ++kb)
+  for (int kb = KB0; kb < KB1; ++kb)
     dma16s(ws, lds0 + unsigned(kDpWOff + st * kDpWst + (kb * 4 + lw) * 1024), w_voff[kb], ws_off);
 }
 
@@ -214,8 +216,9 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
 #pragma unroll
       for (int k = 0; k < KA; ++k) rr[k] = load16s(xs, a_voff[k], as);
     };
+    // steps 2 and later: this loader issues load blocks 0 .. kDpKWh-1 of its weight share, multiplying wave lw the rest
     auto load_step = [&](int t, int st, u32x4 (&rr)[KA]) __attribute__((always_inline)) {
-      load_w(t, st);
+      deep_load_w<0, kDpKWh>(w, g, lds0, lw, w_voff, t, st);
       load_a(t, rr);
     };
     auto write_rows = [&](int st, u32x4 (&rr)[KA]) __attribute__((always_inline)) {
@@ -261,13 +264,12 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
   }
 
   // ====================== multiplying wave w: slices 4t + w ======================
-  // First, step 1's weight share w (the loaders issue every other load of the first two stages): more waves issuing
-  // load instructions move the cold start's bytes from L2 faster
-  {
-    int w_voff[kDpKW];
-    deep_w_offsets(wave, lane, o0, g, w_voff);
-    deep_load_w(w, g, lds0, wave, w_voff, 1, 1);
-  }
+  // First, step 1's weight share w (the loaders issue every other load of the first two stages); from step 2 on this
+  // wave issues load blocks kDpKWh .. kDpKW-1 of that share: more waves with loads in flight move a step's bytes
+  // from L2 faster
+  int w_voff[kDpKW];
+  deep_w_offsets(wave, lane, o0, g, w_voff);
+  deep_load_w(w, g, lds0, wave, w_voff, 1, 1);
   using Sc = DeepSched;
   constexpr int NM = Sc::NM, TL = Sc::TL;
   const int wv = wave;
@@ -328,10 +330,14 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
   for_seq([&](auto pc) __attribute__((always_inline)) { perm_tap(pc); }, std::make_integer_sequence<int, 4 * TL>{});
 
   // step t (u = t mod 2): slice 4t + w multiplies from pixel set u; step t + 1's slice is read from stage 1 - u
-  auto step = [&](auto u_c) __attribute__((always_inline)) {
+  auto step = [&](int tt, auto u_c) __attribute__((always_inline)) {
     constexpr int cur = decltype(u_c)::value, nxt = cur ^ 1;
     using STn = std::integral_constant<int, nxt>;
+    wait_vmcnt<0>();  // this wave's loads into step t + 1's stage (and the bias loads, long landed)
     stage_barrier();  // step t + 1 is in LDS; every wave is done with step t - 1 (and with step t's stage)
+    __builtin_amdgcn_sched_barrier(0);
+    // step t's stage is free: this wave's part of step t + 2's weights
+    if (tt + 2 < g.NS) deep_load_w<kDpKWh, kDpKW>(w, g, lds0, wv, w_voff, tt + 2, cur);
     __builtin_amdgcn_sched_barrier(0);
     for_seq([&](auto kc) __attribute__((always_inline)) {
       constexpr int k = decltype(kc)::value;
@@ -352,10 +358,9 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
       __builtin_amdgcn_sched_barrier(0);
     }, std::make_integer_sequence<int, NM>{});
   };
-  wait_vmcnt<4>();  // this wave's share of step 1's weights (the 4 bias loads after them may be in flight)
   for (int t = 0; t < g.NS; t += 2) {
-    step(I0{});
-    if (t + 1 < g.NS) step(std::integral_constant<int, 1>{});
+    step(t, I0{});
+    if (t + 1 < g.NS) step(t + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- epilogue: tap-column shifts, the four partial tiles added in LDS in wave order, bias + ReLU + one rounding --
