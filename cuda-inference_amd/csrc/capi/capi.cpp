@@ -216,6 +216,23 @@ int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_te
   });
 }
 
+int gie_conv2d_forward_n_timed(const gie_problem* p, const gie_tensor* x, const gie_tensor* w,
+                               const gie_tensor* bias, const gie_tensor* y, void* workspace, size_t workspace_bytes,
+                               void* stream, const gie_options* opt, int count, void* ev_start, void* ev_end) {
+  return guarded([&] {
+    GIE_REQUIRE(ev_start != nullptr && ev_end != nullptr, StatusCode::kInvalidArgument, "null event");
+    const ConstTensorRef b = bias ? to_cref(bias) : ConstTensorRef{};
+    const ConstTensorRef xr = to_cref(x), wr = to_cref(w);
+    const TensorRef yr = to_ref(y);
+    const ConvProblem pr = to_problem(p);
+    const Conv2DOptions o = to_options(opt);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    GIE_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev_start), s));
+    for (int i = 0; i < count; ++i) Conv2D::forward(xr, wr, bias ? &b : nullptr, pr, yr, workspace, workspace_bytes, s, o);
+    GIE_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev_end), s));
+  });
+}
+
 int gie_conv2d_time_forward(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
                             const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
                             const gie_options* opt, int warmup, int samples, double min_sample_ms, double* stats7,

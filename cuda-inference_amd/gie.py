@@ -110,6 +110,7 @@ _CAPI = {
     "gie_problem_key": ([_PP, _cp, _sz], _i),
     "gie_conv2d_forward": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP], _i),
     "gie_conv2d_forward_n": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP, _i], _i),
+    "gie_conv2d_forward_n_timed": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP, _i, _vp, _vp], _i),
     "gie_conv2d_time_forward": ([_PP, _TP, _TP, _TP, _TP, _vp, _sz, _vp, _OP, _i, _i, ctypes.c_double,
                                  ctypes.POINTER(ctypes.c_double), _ip], _i),
     "gie_conv2d_workspace_size": ([_PP, _OP, ctypes.POINTER(_sz)], _i),
@@ -553,6 +554,19 @@ def forward_n(p: Problem, t: ConvTensors, workspace: DeviceBuffer | None, stream
                                       ctypes.byref(b) if b is not None else None, ctypes.byref(y),
                                       workspace.addr if workspace else None, workspace.nbytes if workspace else 0,
                                       stream.h if stream else None, ctypes.byref(oc), count), "Conv2D::forward x n")
+
+
+def forward_n_timed(p: Problem, t: ConvTensors, workspace: DeviceBuffer | None, stream: Stream | None, count: int,
+                    start: "Event", end: "Event", **opt):
+    """forward_n with `start` / `end` recorded on the stream by the library right around the calls (the argument
+    marshalling here happens before the start event)."""
+    pc, oc = p.c(), _opts(**opt)
+    x, w, b, y = t.tensors()
+    check(capi().gie_conv2d_forward_n_timed(ctypes.byref(pc), ctypes.byref(x), ctypes.byref(w),
+                                            ctypes.byref(b) if b is not None else None, ctypes.byref(y),
+                                            workspace.addr if workspace else None,
+                                            workspace.nbytes if workspace else 0, stream.h if stream else None,
+                                            ctypes.byref(oc), count, start.h, end.h), "Conv2D::forward x n (timed)")
 
 
 def time_forward(p: Problem, t: ConvTensors, workspace: DeviceBuffer | None, stream: Stream | None, warmup=5,

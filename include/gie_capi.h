@@ -55,6 +55,13 @@ int gie_conv2d_forward(const gie_problem* p, const gie_tensor* x, const gie_tens
 int gie_conv2d_forward_n(const gie_problem* p, const gie_tensor* x, const gie_tensor* w, const gie_tensor* bias,
                          const gie_tensor* y, void* workspace, size_t workspace_bytes, void* stream,
                          const gie_options* opt, int count);
+/* gie_conv2d_forward_n bracketed by two events (hipEvent_t) recorded on `stream` right before the first call and
+   right after the last, so no host-language work sits inside the timed interval; only enqueues (the caller
+   synchronizes). No counterpart in the reference, whose harness records its events from C++ around the loop
+   (benchmarks/benchmark_main.cpp:55-56). */
+int gie_conv2d_forward_n_timed(const gie_problem* p, const gie_tensor* x, const gie_tensor* w,
+                               const gie_tensor* bias, const gie_tensor* y, void* workspace, size_t workspace_bytes,
+                               void* stream, const gie_options* opt, int count, void* ev_start, void* ev_end);
 /* time_stream_work (timing.h:36-38, the reference's timing.cpp:42-83 protocol) around Conv2D::forward itself:
    `warmup` calls, then `samples` samples of back-to-back forward calls lasting at least min_sample_ms each;
    stats = {median, mean, min, max, p10, p90, stddev} in microseconds per call, *inner = calls per sample. The

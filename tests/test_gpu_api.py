@@ -214,6 +214,26 @@ def test_plan_is_reused_across_calls():
     assert b.compare(b.t.y()).passed()
 
 
+def test_forward_n_timed_brackets_the_calls_with_its_events():
+    """The benchmark's timed step: count forward calls with the start/end events recorded by the library."""
+    p = P(1, 8, 8, 8, 8, 3, 3, 1, 1, 1, 1)
+    b = Bundle(p, 5)
+    ws = gie.DeviceBuffer(gie.workspace_size(p, kernel=K16))
+    s = gie.Stream()
+    e0, e1 = gie.Event(), gie.Event()
+    b.t.poison()
+    gie.forward_n_timed(p, b.t, ws, s, 4, e0, e1, kernel=K16)
+    e1.sync()
+    gie.synchronize()
+    assert e0.elapsed_ms(e1) > 0.0
+    assert b.compare(b.t.y()).passed()
+    x, w, bias, y = b.t.tensors()
+    rc = gie.capi().gie_conv2d_forward_n_timed(ctypes.byref(p.c()), ctypes.byref(x), ctypes.byref(w),
+                                              ctypes.byref(bias), ctypes.byref(y), ws.addr, ws.nbytes, s.h,
+                                              ctypes.byref(gie._opts(kernel=K16)), 1, None, e1.h)
+    assert rc != 0 and "null event" in gie.capi().gie_last_error().decode()
+
+
 def test_cost_model_bounds():
     big = P(32, 256, 28, 28, 256, 3, 3, 1, 1, 1, 1)
     assert gie.estimate(K16_BIG, big)["bound"] == "compute"
