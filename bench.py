@@ -323,6 +323,41 @@ def copy_probe(gie, mib: int, reps: int):
     print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": reps}), flush=True)
 
 
+def stream_probe(gie, reps: int = 30, workgroups: int = 256):
+    """HBM streaming ceilings at the benchmark outputs' byte counts (gie_hip_ceiling_stream: one contiguous chunk
+    per workgroup, 16-byte accesses): writes of config 4's Y and the stem's and the pointwise kernel's read+write
+    mixes, per store policy; microseconds per launch from events around `reps` launches after 5 untimed ones."""
+    y4 = 64 * 64 * 112 * 112 * 2
+    cases = [("write c4 Y", 0, y4, (0, 1, 2)),
+             ("stem mix: read x, write Y (c4)", 64 * 3 * 224 * 224 * 2, y4, (0, 1)),
+             ("pointwise mix: c3's counted bytes", 32899072, 116391936, (0, 1)),
+             ("copy-like 64 MiB + 64 MiB", 64 << 20, 64 << 20, (0, 1))]
+    big = max(max(r, w) for _, r, w, _ in cases)
+    src, dst = gie.DeviceBuffer(big), gie.DeviceBuffer(big)
+    src.fill(0x3C)
+    dst.fill(0)
+    s = gie.Stream()
+    e0, e1 = gie.Event(), gie.Event()
+    names = {0: "write-back", 1: "device scope (sc1)", 2: "non-temporal"}
+    out = []
+    for name, rb, wb, pols in cases:
+        for pol in pols:
+            launch = lambda: gie.check_hip(gie.hip().gie_hip_ceiling_stream(src.addr if rb else None, rb, dst.addr, wb,
+                                                                              pol, workgroups, s.h), "ceiling_stream")
+            for _ in range(5):
+                launch()
+            e0.record(s)
+            for _ in range(reps):
+                launch()
+            e1.record(s)
+            e1.sync()
+            us = e0.elapsed_ms(e1) * 1e3 / reps
+            out.append({"case": name, "stores": names[pol], "read_bytes": rb, "write_bytes": wb, "us": us,
+                        "tb_per_s": (rb + wb) / us / 1e6})
+            log(f"stream probe: {name}, {names[pol]}: {us:.2f} us, {(rb + wb) / us / 1e6:.2f} TB/s")
+    print(json.dumps({"stream_probe": out, "workgroups": workgroups, "threads": 512, "launches": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -337,6 +372,8 @@ def main():
                          "than the headline only that config runs and its result dict is printed (profiling runs)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="only run the HBM streaming ceilings (write / read / read+write per store policy) and exit")
     args = ap.parse_args()
     if args.steps < 1 or args.warmup < 0:
         ap.error("--steps must be >= 1 and --warmup >= 0")
@@ -349,6 +386,9 @@ def main():
     import gie
     gie.check(gie.capi().gie_set_device(0), "hipSetDevice")
     os.makedirs(os.path.dirname(args.tune_cache), exist_ok=True)
+    if args.stream_probe:
+        stream_probe(gie)
+        return
     if args.copy_probe_mib > 0:
         copy_probe(gie, args.copy_probe_mib, 5)
         return

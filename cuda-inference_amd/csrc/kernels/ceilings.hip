@@ -38,6 +38,39 @@ __global__ __launch_bounds__(256) void fill_u16_kernel(uint16_t* __restrict__ ds
     dst[i] = v;
 }
 
+// Streaming probe: workgroup b reads its own r16 16-byte elements of src and writes its own w16 elements of dst
+// (contiguous chunks), 512 elements per step; the reads are spread evenly over the steps. POL: 0 write-back
+// stores, 1 device scope (sc1, written through the L2), 2 non-temporal.
+template <int POL>
+__device__ __forceinline__ void stream_store(u32x4* p, u32x4 v) {
+  if constexpr (POL == 0)
+    asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
+  else if constexpr (POL == 1)
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
+  else
+    asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
+}
+template <int POL>
+__global__ __launch_bounds__(512) void stream_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                     long long r16, long long w16) {
+  const long long rb = static_cast<long long>(blockIdx.x) * r16, wb = static_cast<long long>(blockIdx.x) * w16;
+  const int t = threadIdx.x, nt = blockDim.x;
+  const long long ws = (w16 + nt - 1) / nt, rs = (r16 + nt - 1) / nt, steps = ws > rs ? ws : rs;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (long long s = 0; s < steps; ++s) {
+    const long long k = s * rs / steps;
+    if (k != (s + 1) * rs / steps) {  // read step k (each of the rs read steps exactly once)
+      const long long i = k * nt + t;
+      if (i < r16) acc += src[rb + i];
+    }
+    if (s < ws) {
+      const long long i = s * nt + t;
+      if (i < w16) stream_store<POL>(dst + wb + i, u32x4{acc.x, unsigned(s), unsigned(t), 7u});
+    }
+  }
+  if (acc.x == 0x9876543u && acc.y == 17u) dst[0] = acc;  // practically never true: keeps the reads
+}
+
 int launched() {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GIE_HIP_OK : int(e);
@@ -63,6 +96,21 @@ extern "C" int gie_hip_ceiling_copy(const void* src, void* dst, size_t bytes, vo
   if (blocks > static_cast<long long>(cus) * 16) blocks = static_cast<long long>(cus) * 16;
   hipLaunchKernelGGL(copy_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), n);
+  return launched();
+}
+
+extern "C" int gie_hip_ceiling_stream(const void* src, size_t read_bytes, void* dst, size_t write_bytes,
+                                      int store_policy, int workgroups, void* stream) {
+  if (workgroups <= 0 || store_policy < 0 || store_policy > 2 || !dst || (read_bytes > 0 && !src) ||
+      (read_bytes == 0 && write_bytes == 0))
+    return GIE_HIP_EINVAL;
+  const size_t unit = 16 * static_cast<size_t>(workgroups);
+  if (read_bytes % unit != 0 || write_bytes % unit != 0) return GIE_HIP_EINVAL;
+  using Fn = void (*)(const u32x4*, u32x4*, long long, long long);
+  const Fn fns[3] = {&stream_kernel<0>, &stream_kernel<1>, &stream_kernel<2>};
+  hipLaunchKernelGGL(fns[store_policy], dim3(unsigned(workgroups)), dim3(512), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(src), static_cast<u32x4*>(dst),
+                     static_cast<long long>(read_bytes / unit), static_cast<long long>(write_bytes / unit));
   return launched();
 }
 

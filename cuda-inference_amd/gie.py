@@ -231,6 +231,7 @@ _HIP = {
     "gie_hip_reference_conv": ([_i, _GP, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "gie_hip_ceiling_mfma": ([_i, _i, _vp, _vp], _i),
     "gie_hip_ceiling_copy": ([_vp, _vp, _sz, _vp], _i),
+    "gie_hip_ceiling_stream": ([_vp, _sz, _vp, _sz, _i, _i, _vp], _i),
     "gie_hip_ceiling_empty": ([_vp], _i),
     "gie_hip_ceiling_empty_args": ([_i, _vp], _i),
     "gie_hip_fill_u16": ([_vp, ctypes.c_int64, ctypes.c_uint16, _vp], _i),

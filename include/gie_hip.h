@@ -338,6 +338,14 @@ int gie_hip_ceiling_empty(void* stream);
    function of its kernel arguments (HIP copies a non-empty block to device memory by default). GIE_HIP_EINVAL for
    other sizes. No counterpart in the reference: a measurement of this build's launch path. */
 int gie_hip_ceiling_empty_args(int arg_bytes, void* stream);
+/* HBM streaming probe: `workgroups` workgroups of 512 threads, workgroup b reading its own contiguous read_bytes /
+   workgroups of src and writing its own write_bytes / workgroups of dst in 16-byte lane accesses (reads spread evenly
+   over the writes); store_policy 0 write-back, 1 device scope (written through the L2), 2 non-temporal. Both sizes
+   multiples of 16 * workgroups; dst is required (with write_bytes 0 it only receives a never-taken sink store). No
+   counterpart in the reference: the write and read/write ceilings the stem and pointwise kernels are measured
+   against. */
+int gie_hip_ceiling_stream(const void* src, size_t read_bytes, void* dst, size_t write_bytes, int store_policy,
+                           int workgroups, void* stream);
 
 /* dst[i] = value for i < n (16-bit elements, any 2-byte alignment). A graph-safe fill (no memset node). */
 int gie_hip_fill_u16(void* dst, int64_t n, uint16_t value, void* stream);

@@ -6,7 +6,8 @@
 * MFMA implicit GEMM: every registered kernel on the reference's 26 correctness shapes (tests/shapes.h) in
   FP16 and BF16, cycling epilogues and distributions like run_suite (tests/conv_test_common.h:83-127), against
   the reference's per-element tolerance; every (shape, precision) cell must be covered by >= 1 kernel;
-* the library's GPU double reference against the oracle (tests/test_direct_conv.cpp:6-21).
+* the library's GPU double reference against the oracle (tests/test_direct_conv.cpp:6-21);
+* the HBM streaming probe behind the measured write/read ceilings: layout of its writes and its argument checks.
 """
 import ctypes
 
@@ -197,3 +198,42 @@ def _repeat_check(k, b):
     for _ in range(3):
         again, _ = run_plan(k, b, repeats=2)
         assert np.array_equal(first.view(np.uint32), again.view(np.uint32)), k
+
+
+@pytest.mark.parametrize("policy", [0, 1, 2])
+def test_stream_ceiling_writes_each_workgroups_own_chunk(policy):
+    """gie_hip_ceiling_stream: workgroup b writes exactly its own chunk, element s*512 + t of it (step s, thread t)
+    holding (sum of what it read, s, t, 7); a read-only run leaves dst untouched."""
+    h = gie.hip()
+    wg, w16 = 4, 3 * 512 + 64  # per workgroup: 3 whole steps and a partial one
+    r16 = 512 + 40
+    src = gie.DeviceBuffer(wg * r16 * 16)
+    src.fill(0)
+    dst = gie.DeviceBuffer(wg * w16 * 16 + 64)
+    dst.fill(0xAB)
+    gie.check_hip(h.gie_hip_ceiling_stream(src.addr, wg * r16 * 16, dst.addr, wg * w16 * 16, policy, wg, None),
+                  "ceiling_stream")
+    gie.synchronize()
+    out = dst.download(np.uint32, (wg * w16 * 16 + 64) // 4)
+    got = out[:wg * w16 * 4].reshape(wg, w16, 4)
+    i = np.arange(w16)
+    want = np.stack([np.zeros(w16, np.uint32), (i // 512).astype(np.uint32), (i % 512).astype(np.uint32),
+                     np.full(w16, 7, np.uint32)], axis=1)
+    for b in range(wg):
+        assert np.array_equal(got[b], want), b
+    assert np.all(out[wg * w16 * 4:] == 0xABABABAB)  # nothing past the last chunk
+    dst.fill(0xAB)
+    gie.check_hip(h.gie_hip_ceiling_stream(src.addr, wg * r16 * 16, dst.addr, 0, policy, wg, None), "read only")
+    gie.synchronize()
+    assert np.all(dst.download(np.uint32, 16) == 0xABABABAB)
+
+
+def test_stream_ceiling_argument_checks():
+    h = gie.hip()
+    d = gie.DeviceBuffer(1 << 16)
+    assert h.gie_hip_ceiling_stream(d.addr, 4096, d.addr, 4096, 3, 16, None) != 0      # policy
+    assert h.gie_hip_ceiling_stream(d.addr, 4096, d.addr, 4096, 0, 0, None) != 0      # workgroups
+    assert h.gie_hip_ceiling_stream(d.addr, 4096 + 16, d.addr, 4096, 0, 16, None) != 0  # not a multiple of 16 * wg
+    assert h.gie_hip_ceiling_stream(None, 4096, d.addr, 4096, 0, 16, None) != 0        # reads without src
+    assert h.gie_hip_ceiling_stream(d.addr, 4096, None, 0, 0, 16, None) != 0           # no dst
+    assert h.gie_hip_ceiling_stream(d.addr, 0, d.addr, 0, 0, 16, None) != 0            # nothing to do
