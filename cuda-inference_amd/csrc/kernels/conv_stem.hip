@@ -14,7 +14,7 @@
 //     one image (R * out_w pixels, contiguous in each output plane). The tile's 2R+5 input rows per channel sit in LDS with 4 zero
 //     dwords on each side (the horizontal padding); rows above or below the image are loaded as zeros. Wave 7
 //     streams rows: tile i+2's rows go straight into the third of three row buffers (buffer_load ... lds) while
-//     waves 0..6 multiply tile i. Waves 0..6 hold the 64 filters' operands in registers (2 x 32 columns x K);
+//     waves 0..6 multiply tile i (tile 0's rows come from waves 0..6 at the start, tile 1's from wave 7). Waves 0..6 hold the 64 filters' operands in registers (2 x 32 columns x K);
 //     per 32-pixel block: two ds_read2_b32 and one AND per k-step, two MFMA chains. One barrier per tile.
 //   * MFMA roles: rows = pixels, columns = filters, so each lane's accumulators hold 4-pixel runs of one filter.
 //     Epilogue: ReLU, RNE rounding (the order of the reference's apply_epilogue,
@@ -129,9 +129,19 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
         }
     }
   };
+  // tile 0's rows come from the multiplying waves (row q to wave q % 7, issued before their weight loads and waited
+  // with them), tile 1's from the streaming wave, so the first tile's 39 loads are not issued by one wave
   if (wave == kStLoader) {
-    if (n_my > 0) load_rows(0);
     if (n_my > 1) load_rows(1);
+  } else if (n_my > 0 && lane < g.CPR) {
+    const int n = t0 / g.n_rt, oh0 = (t0 - n * g.n_rt) * R;
+    unsigned char* dst = rows(0) + kStPad * 4;
+    for (int q = wave; q < NROW; q += kStCW) {
+      const int c = q / WR, lr = q - c * WR;
+      const int ih = 2 * oh0 - 3 + lr;
+      const int voff = ih >= 0 && ih < g.H ? ((n * C + c) * g.H + ih) * row_bytes + lane * 16 : kOut;
+      dma16(xr, lds_addr(dst + (c * WR + lr) * g.RS * 4), voff);
+    }
   }
   // the horizontal padding of every row buffer: zero once, never written again
   for (int idx = tid; idx < kStBufs * NROW * 8; idx += kStNT) {
@@ -184,9 +194,7 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   if (wave == kStLoader) {
     // ---- streaming wave: before the barrier that ends tile i, tile i+1's rows must have landed; tile i+2's are
     // issued first and may stay in flight (this wave issues no other vector-memory operation in the loop)
-    if (n_my > 1) wait_vm<NROW>();  // tile 0's rows are in; tile 1's may be in flight
-    else wait_vm<0>();
-    stage_barrier();
+    stage_barrier();  // B0 (tile 0's rows: the multiplying waves waited for them; tile 1's may be in flight)
     for (int i = 0; i < n_my; ++i) {
       if (i + 2 < n_my) {
         load_rows(i + 2);
