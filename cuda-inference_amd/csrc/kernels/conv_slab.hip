@@ -1048,6 +1048,58 @@ struct SplitSched {
   static_assert(B_BEG < L_BEG && late_slot(NLATE - 1) < NM, "slot plan");
 };
 
+// The direct-to-LDS loads of loader share lw (0..3) of a slice: KA activation blocks (8 channels' rows, two channel
+// regions per 16-byte load) and KBW weight blocks, as the pipelined form's wave lw issues them; slices past the unit's
+// last load through zero-length resources (every step counts the same loads).
+template <int P, int NBW, int NST>
+struct SplitShare {
+  using Sh = SlabShape<P, NBW, NST>;
+  static constexpr int CS = Sh::CS, NW = Sh::NW, NR = Sh::NR, CPF = Sh::CPF, WCH = Sh::WCH, KBW = Sh::KBW;
+  static constexpr int ACT = Sh::ACT, WST = Sh::WST, WOFF = NST * ACT, KA = ACT / 1024 / NW;
+  v4i xr, wrs, x0, w0;
+  int w_voff[KBW], a_voff[2];
+  int hw2, a_soff0, w_soff0, lw, ns;
+  unsigned lds0;
+  __device__ __forceinline__ SplitShare(const uint16_t* x, const uint16_t* w, const SlabGeom& g, int lw_, int lane, int b,
+                                        int o0, int oh0, int s_beg, int ns_, unsigned lds0_)
+      : lw(lw_), ns(ns_), lds0(lds0_) {
+    xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
+    x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: loads give zeros
+    const int wrow = g.C * 18;  // bytes of one filter's OIHW weights
+#pragma unroll
+    for (int kb = 0; kb < KBW; ++kb) {
+      const int u = (lw + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
+      const int val = (o0 + f) * wrow + 16 * k;
+      const bool ok = (f < kSlTO) & (k < WCH) & (o0 + f < g.O);
+      w_voff[kb] = ok ? val : kOut;
+    }
+    const int cl = lane >> 5, sslot = (lane >> 1) & 15, half = lane & 1;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int pos = ((sslot ^ seg_swz(8 * lw + 2 * e + cl)) << 4) + 8 * half;
+      const int row = pos / P, col = pos % P, ih = oh0 - 1 + row;
+      const int val = (cl * g.HW + ih * g.W + col) * 2;
+      const bool ok = (row < NR) & (unsigned(ih) < unsigned(g.H)) & (col < g.W);
+      a_voff[e] = ok ? val : kOut;
+    }
+    hw2 = g.HW * 2;
+    a_soff0 = (b * g.C + s_beg * CS + 8 * lw) * hw2;
+    w_soff0 = s_beg * CS * 18;
+  }
+  // load q of slice s into stage st: q < KA the share's activation rows, then its weight blocks
+  __device__ __forceinline__ void issue(int s, int st) const {
+    const bool real = s < ns;
+    const v4i xs = real ? xr : x0, ws = real ? wrs : w0;
+    const int a_soff = real ? a_soff0 + s * CS * hw2 : 0, w_soff = real ? w_soff0 + s * CS * 18 : 0;
+#pragma unroll
+    for (int q = 0; q < KA; ++q)
+      dma16s(xs, lds0 + unsigned(st * ACT + (lw * KA + q) * 1024), a_voff[q & 1], a_soff + 2 * q * hw2);
+#pragma unroll
+    for (int kb = 0; kb < KBW; ++kb)
+      dma16s(ws, lds0 + unsigned(WOFF + st * WST + (lw + NW * kb) * 1024), w_voff[kb], w_soff);
+  }
+};
+
 template <typename E, int P, int NBW, int NST>
 __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ w,
@@ -1055,8 +1107,8 @@ __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __re
                                                            float* __restrict__ partial, SlabGeom g) {
   using Sh = SlabShape<P, NBW, NST>;
   using Sc = SplitSched<P, NBW>;
-  constexpr int CS = Sh::CS, NW = Sh::NW, RW = Sh::RW, RB = Sh::RB, NR = Sh::NR, G = Sh::G, NBR = Sh::NBR;
-  constexpr int CPF = Sh::CPF, WCH = Sh::WCH, WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
+  constexpr int NW = Sh::NW, RW = Sh::RW, RB = Sh::RB, G = Sh::G, NBR = Sh::NBR;
+  constexpr int WPITCH = Sh::WPITCH, KBW = Sh::KBW, WST = Sh::WST, CHP = Sh::CHP;
   constexpr int ACT = Sh::ACT;
   constexpr int WOFF = NST * ACT;      // LDS: [NST activation stages][NST weight stages]
   constexpr int KA = ACT / 1024 / NW;  // 16-byte activation loads per loader per slice, two channel regions each
@@ -1086,60 +1138,19 @@ __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __re
 
   if (wave >= NW) {
     // ================= loader wave lw = wave - NW: the loads the pipelined form's wave lw issues =================
-    const int lw = wave - NW;
-    const v4i xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
-    const v4i x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: loads give zeros
-    int w_voff[KBW];
-    const int wrow = g.C * 18;  // bytes of one filter's OIHW weights
-#pragma unroll
-    for (int kb = 0; kb < KBW; ++kb) {
-      const int u = (lw + NW * kb) * 64 + lane, f = u / CPF, k = u - f * CPF;
-      const int val = (o0 + f) * wrow + 16 * k;
-      const bool ok = (f < kSlTO) & (k < WCH) & (o0 + f < g.O);
-      w_voff[kb] = ok ? val : kOut;
-    }
-    int a_voff[2];
-    {
-      const int cl = lane >> 5, sslot = (lane >> 1) & 15, half = lane & 1;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int pos = ((sslot ^ seg_swz(8 * lw + 2 * e + cl)) << 4) + 8 * half;
-        const int row = pos / P, col = pos % P, ih = oh0 - 1 + row;
-        const int val = (cl * g.HW + ih * g.W + col) * 2;
-        const bool ok = (row < NR) & (unsigned(ih) < unsigned(g.H)) & (col < g.W);
-        a_voff[e] = ok ? val : kOut;
-      }
-    }
-    const int hw2 = g.HW * 2;
-    const int a_soff0 = (b * g.C + s_beg * CS + 8 * lw) * hw2;
-    const int w_soff0 = s_beg * CS * 18;
-    // load q of slice s into stage st: q < KA this loader's activation rows, then its weight blocks; slices past the
-    // unit's last load through zero-length resources (every step counts the same loads)
-    auto load_slice = [&](int s, int st) __attribute__((always_inline)) {
-      const bool real = s < ns;
-      const v4i xs = real ? xr : x0, ws = real ? wrs : w0;
-      const int a_soff = real ? a_soff0 + s * CS * hw2 : 0, w_soff = real ? w_soff0 + s * CS * 18 : 0;
-#pragma unroll
-      for (int q = 0; q < KA; ++q)
-        dma16s(xs, lds0 + unsigned(st * ACT + (lw * KA + q) * 1024), a_voff[q & 1], a_soff + 2 * q * hw2);
-#pragma unroll
-      for (int kb = 0; kb < KBW; ++kb)
-        dma16s(ws, lds0 + unsigned(WOFF + st * WST + (lw + NW * kb) * 1024), w_voff[kb], w_soff);
-    };
-    // slices 0 and 1 first, so the first slice shares the cold start's bandwidth with one other slice, not two;
-    // slice 2 goes out once slice 0 has landed
-    static_assert(NST == 3, "the start-up sequence below issues slices 0, 1 and then 2");
-    load_slice(0, 0);
-    load_slice(1, 1);
-    wait_vmcnt<NI>();  // slice 0
-    stage_barrier();   // B0: slice 0 is in LDS
-    load_slice(2, 2);
-    wait_vmcnt<NI>();  // slice 1
-    stage_barrier();   // start of step 0
+    const SplitShare<P, NBW, NST> ld(x, w, g, wave - NW, lane, b, o0, oh0, s_beg, ns, lds0);
+    // slice 0 first (slice 1 is the multiplying waves': each issues its partner loader's share at its start, so
+    // eight waves load the cold start's two slices); slice 2 goes out once slice 0 has landed
+    static_assert(NST == 3, "the start-up sequence below issues slices 0 and then 2 (slice 1: the multiplying waves)");
+    ld.issue(0, 0);
+    wait_vmcnt<0>();  // slice 0
+    stage_barrier();  // B0: slice 0 is in LDS
+    ld.issue(2, 2);
+    stage_barrier();  // start of step 0 (slice 1: the multiplying waves waited for their loads)
     for (int j = 0; j + 1 < ns; ++j) {
       // step j: slice j was read in step j - 1, so its stage takes slice j + NST; slice j + 2 must land before the
       // barrier that starts step j + 1
-      load_slice(j + NST, j % NST);
+      ld.issue(j + NST, j % NST);
       wait_vmcnt<(NST - 2) * NI>();
       stage_barrier();
     }
@@ -1148,6 +1159,10 @@ __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __re
   }
 
   // ================= multiplying wave: (filter half fh, row half wr) =================
+  {  // first, slice 1's share `wave` (its partner loader issues slice 0 and the later slices)
+    const SplitShare<P, NBW, NST> ld(x, w, g, wave, lane, b, o0, oh0, s_beg, ns, lds0);
+    ld.issue(1, 1);
+  }
   const int fh = wave & 1, wr = wave >> 1;
   const int nrows = min(RB, g.H - oh0);
   const int f0 = o0 + fh * 16 + 4 * (lane >> 4);
@@ -1235,6 +1250,7 @@ __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __re
       __builtin_amdgcn_sched_barrier(0);
     }, std::make_integer_sequence<int, NM>{});
   };
+  wait_vmcnt<4>();  // this wave's share of slice 1 (the 4 bias loads after it may be in flight)
   for (int j = 0; j < ns; j += U) {
     for_seq([&](auto uc) __attribute__((always_inline)) {
       if (j + decltype(uc)::value < ns) step(uc);
