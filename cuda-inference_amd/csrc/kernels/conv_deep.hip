@@ -180,13 +180,12 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
   if (wave >= 4) {
     // ====================== loader wave lw = wave - 4 (lt = its thread index among the loaders) ======================
     const int lw = wave - 4, lt = tid - 256;
-    const v4i xr = make_vsharp(x, g.x_bytes), wrs = make_vsharp(w, g.w_bytes);
-    const v4i x0 = make_vsharp(x, 0), w0 = make_vsharp(w, 0);  // every offset out of range: zeros, no traffic
+    const v4i xr = make_vsharp(x, g.x_bytes);
+    const v4i x0 = make_vsharp(x, 0);  // every offset out of range: zeros, no traffic
     int w_voff[kDpKW];
     deep_w_offsets(lw, lane, o0, g, w_voff);
     const int a_step = kDpQ * kDpCS * g.HW * 2;
-    auto load_w = [&](int t, int st) __attribute__((always_inline)) { deep_load_w(w, g, lds0, lw, w_voff, t, st); };
-    load_w(0, 0);  // the first loads leave before any other set-up work
+    deep_load_w<0, kDpKWh>(w, g, lds0, lw, w_voff, 0, 0);  // the first loads leave before any other set-up work
     __builtin_amdgcn_sched_barrier(0);
     // activation item e = k * 256 + lt: (channel ch of the step's 128, row r); the row's W halves start at element
     // (b * C + ch) * HW + r * W; the load starts at the 4-byte boundary at or below it
@@ -264,11 +263,12 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
   }
 
   // ====================== multiplying wave w: slices 4t + w ======================
-  // First, step 1's weight share w (the loaders issue every other load of the first two stages); from step 2 on this
-  // wave issues load blocks kDpKWh .. kDpKW-1 of that share: more waves with loads in flight move a step's bytes
-  // from L2 faster
+  // First, load blocks kDpKWh .. kDpKW-1 of step 0's weight share w and all of step 1's (the loaders issue every
+  // other load of the first two stages); from step 2 on this wave issues load blocks kDpKWh .. kDpKW-1 of that share:
+  // more waves with loads in flight move a step's bytes from L2 faster
   int w_voff[kDpKW];
   deep_w_offsets(wave, lane, o0, g, w_voff);
+  deep_load_w<kDpKWh, kDpKW>(w, g, lds0, wave, w_voff, 0, 0);  // the second half of step 0's share
   deep_load_w(w, g, lds0, wave, w_voff, 1, 1);
   using Sc = DeepSched;
   constexpr int NM = Sc::NM, TL = Sc::TL;
@@ -322,6 +322,7 @@ __global__ __launch_bounds__(kDpNT, 1) void deep_kernel(const uint16_t* __restri
   };
   using I0 = std::integral_constant<int, 0>;
 
+  wait_vmcnt<kDpKW + 4>();  // this wave's half of step 0's weights (step 1's and the 4 bias loads may be in flight)
   stage_barrier();  // B0: step 0 in LDS
   // step 0's slice into registers: its weight runs, its pixel fragments (set 0), the transposes of taps 0 .. TL-1
   for_seq([&](auto qc) __attribute__((always_inline)) { read_w(qc, I0{}); }, std::make_integer_sequence<int, 9>{});
