@@ -93,6 +93,9 @@ CASES = [
     (1, 32, 10, 10, 32, "fp16", True, True, 1, 0, 0),     # one slice: fewer slices than load stages
     (2, 96, 12, 14, 64, "bf16", True, True, 2, 0, 0),     # split-K 2 over 3 slices (ranges of 1 and 2)
     (3, 320, 14, 8, 72, "fp16", True, False, 1, 0, 0),    # 10 slices: a partial loop turn, O past two blocks
+    (2, 96, 14, 12, 64, "bf16", True, False, 1, 0, 0),    # 3 slices (one loop turn short), no ReLU, two blocks
+    (1, 160, 9, 10, 64, "fp16", False, True, 1, 0, 0),    # 5 slices, image shorter than the slab
+    (2, 64, 14, 14, 32, "fp16", True, True, 1, 0, 8),     # y offset by 8 bytes: pixel-pair stores
 ]
 
 
