@@ -18,8 +18,10 @@
 //     per 32-pixel block: two ds_read2_b32 and one AND per k-step, two MFMA chains. One barrier per tile.
 //   * MFMA roles: rows = pixels, columns = filters, so each lane's accumulators hold 4-pixel runs of one filter.
 //     Epilogue: ReLU, RNE rounding (the order of the reference's apply_epilogue,
-//     src/kernels/fused_epilogue.cuh:11-16), the wave's 64-filter x 32-pixel tile staged in LDS, 16-byte stores
-//     with every 4 lanes writing one 64-byte run of a filter's output row.
+//     src/kernels/fused_epilogue.cuh:11-16), then the wave's two adjacent 32-pixel blocks staged in LDS as one
+//     64-filter x 64-pixel tile and written by 16-byte stores, every 8 lanes one 128-byte run of a filter's output
+//     row (whole lines: a tile starts on a 128-byte boundary of each plane when R * out_w * 2 and the plane size are
+//     multiples of 128). Where the LDS cannot hold an 8 KiB tile per wave, one block at a time in 64-byte runs.
 //   * Grid: one 8-wave workgroup per CU; tiles are split into 8 contiguous ranges, one per XCD (blockIdx mod 8),
 //     so the input rows shared by neighbouring tiles are read into one L2.
 #include <algorithm>
@@ -48,7 +50,8 @@ struct StemGeom {
   int RS;         // LDS row stride in dwords: in_w / 2 + 8
   int buf_bytes;  // one row buffer: C * WR * RS * 4
   int rows_off;   // LDS byte offset of the row buffers (after the MFMA operands)
-  int tile_off;   // LDS byte offset of the multiplying waves' output tiles (4 KiB each)
+  int tile_off;   // LDS byte offset of the multiplying waves' output tiles (8 KiB each, 4 KiB without `wide`)
+  int wide;       // 128-byte output runs: each wave takes two adjacent 32-pixel blocks (host-side choice)
   int x_bytes, y_bytes;
 };
 
@@ -85,7 +88,7 @@ constexpr uint32_t one_bits() {
   return E::kDtype == GIE_HIP_FP16 ? 0x3C00u : 0x3F80u;
 }
 
-template <typename E, int C, int R, bool RELU>
+template <typename E, int C, int R, bool RELU, bool WIDE>
 __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
                                                     StemGeom g) {
@@ -221,29 +224,49 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
   const int h_next = hi * rs4, h_chan = hi * (WR - 6) * rs4;
   stage_barrier();  // tile 0's rows are in
 
-  // ---- multiplying waves: 32-pixel blocks of tile i from row buffer i % 3, in pairs (wave, wave + 7), (wave + 14,
-  // wave + 21), ...: the second block's rows are read before the first block's stores are issued
+  // ---- multiplying waves: 32-pixel blocks of tile i from row buffer i % 3, two at a time (below)
   const int npix = R * g.OW;
   const float inv_ow = 1.0f / float(g.OW);
-  // Output tile of this wave in LDS: row r (64 bytes) holds filter f0 + r; its 8-byte granule q sits at
-  // q ^ (2 * ((r / 4) & 3)). Writes: lane (hi, col) puts pixels 8a + 4hi .. +3 of filter 32fh + col into granule
+  // Output tile of this wave in LDS.
+  // 64-byte runs (!WIDE, one 32-pixel block at a time): row r (64 bytes) holds filter f0 + r; its 8-byte granule q sits
+  // at q ^ (2 * ((r / 4) & 3)). Writes: lane (hi, col) puts pixels 8a + 4hi .. +3 of filter 32fh + col into granule
   // 2a + hi of row 32fh + col. Reads: read t of lane l covers row 16t + l/4, 16-byte segment l%4 (stored at
   // segment (l%4) ^ ((l/16) & 3)).
+  // 128-byte runs (WIDE, two adjacent blocks): row r (128 bytes) holds filter f0 + r for the pair's 64 pixels; its
+  // 16-byte segment s (pixels 8s .. 8s+7) sits at s ^ ((r / 2) & 7). Writes: lane (hi, col) puts pixels 8a + 4hi .. +3
+  // of block bh into the 8-byte half hi of segment 4bh + a of row 32fh + col (2-way bank conflict, as above). Reads:
+  // read t of lane l covers row 8t + l/8, segment l%8, stored at (l%8) ^ ((l/16) + 4 (t%2)) (conflict-free).
+  constexpr unsigned kTB = WIDE ? 8192u : 4096u;
   typedef __attribute__((address_space(3))) u32x2 lds_u32x2_t;
   typedef __attribute__((address_space(3))) const u32x4 lds_cu32x4_t;
-  const unsigned stg = lds_addr(smem + g.tile_off) + unsigned(wave) * 4096u;
-  lds_u32x2_t* w_q[4];
+  const unsigned stg = lds_addr(smem + g.tile_off) + unsigned(wave) * kTB;
+  constexpr int NQ = WIDE ? 8 : 4;  // write pointers: one per (block, a) segment
+  lds_u32x2_t* w_q[NQ];
+  lds_cu32x4_t* r_base[WIDE ? 2 : 1];
+  if constexpr (WIDE) {
+    const unsigned m = (unsigned(col) >> 1) & 7u;
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
-    w_q[a] = reinterpret_cast<lds_u32x2_t*>(size_t(
-        stg + unsigned(col) * 64u + (((unsigned(a) ^ ((unsigned(lane) >> 2) & 3u)) << 1 | unsigned(hi)) << 3)));
-  lds_cu32x4_t* const r_base = reinterpret_cast<lds_cu32x4_t*>(
-      size_t(stg + (unsigned(lane) >> 2) * 64u + (((unsigned(lane) & 3u) ^ ((unsigned(lane) >> 4) & 3u)) << 4)));
-  int f_off[4];  // byte offset of the filter plane of each read's row
-  bool f_ok[4];
+    for (int q = 0; q < NQ; ++q)
+      w_q[q] = reinterpret_cast<lds_u32x2_t*>(
+          size_t(stg + unsigned(col) * 128u + ((unsigned(q) ^ m) << 4) + (unsigned(hi) << 3)));
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int f = f0 + 16 * t + (lane >> 2);
+    for (int par = 0; par < 2; ++par)
+      r_base[par] = reinterpret_cast<lds_cu32x4_t*>(size_t(
+          stg + (unsigned(lane) >> 3) * 128u + (((unsigned(lane) & 7u) ^ ((unsigned(lane) >> 4) + 4u * par)) << 4)));
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      w_q[a] = reinterpret_cast<lds_u32x2_t*>(size_t(
+          stg + unsigned(col) * 64u + (((unsigned(a) ^ ((unsigned(lane) >> 2) & 3u)) << 1 | unsigned(hi)) << 3)));
+    r_base[0] = reinterpret_cast<lds_cu32x4_t*>(
+        size_t(stg + (unsigned(lane) >> 2) * 64u + (((unsigned(lane) & 3u) ^ ((unsigned(lane) >> 4) & 3u)) << 4)));
+  }
+  constexpr int NS = WIDE ? 8 : 4;  // store instructions per tile of the wave: rows per read, 16 (64-byte) or 8
+  int f_off[NS];                    // byte offset of the filter plane of each read's row
+  bool f_ok[NS];
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    const int f = f0 + (WIDE ? 8 * t + (lane >> 3) : 16 * t + (lane >> 2));
     f_ok[t] = f < g.O;
     f_off[t] = int(size_t(f_ok[t] ? f : 0) * y_plane * 2);
   }
@@ -290,40 +313,75 @@ __global__ __launch_bounds__(kStNT) void stem_kernel(const uint16_t* __restrict_
     // faster than 16-byte runs of 32 filters per instruction straight from the registers). The stores are
     // device-scope (store16_wt): 24.5 us per launch on the 64 x 3 x 224 x 224 stem against 25.7 with stores that
     // leave dirty L2 lines to be written back at the end of the launch.
-    auto store = [&](int blk, const f32x16& acc0, const f32x16& acc1) {
+    // the rounded 64 x 32 tile of block half bh (WIDE) or of the block into the wave's LDS tile
+    auto stage = [&](int bh, const f32x16& acc0, const f32x16& acc1) {
 #pragma unroll
       for (int fh = 0; fh < 2; ++fh) {
         const f32x16& acc = fh ? acc1 : acc0;
 #pragma unroll
         for (int a = 0; a < 4; ++a)
-          w_q[a][fh * 256] = u32x2{relu2<E, RELU>(acc[4 * a], acc[4 * a + 1]), relu2<E, RELU>(acc[4 * a + 2], acc[4 * a + 3])};
+          w_q[WIDE ? 4 * bh + a : a][fh * (WIDE ? 512 : 256)] =  // + 32 rows for the second 32-filter half
+              u32x2{relu2<E, RELU>(acc[4 * a], acc[4 * a + 1]), relu2<E, RELU>(acc[4 * a + 2], acc[4 * a + 3])};
       }
       // the tile is written as 8-byte and read as 16-byte vectors: keep the compiler from reordering them (the
       // wave's LDS accesses complete in issue order)
       asm volatile("" ::: "memory");
-      u32x4 v[4];
+    };
+    // the staged tile to y: 16-byte stores, every 4 (8 when WIDE) lanes one 64- (128-) byte run of a filter's output
+    // row; px0 = the tile's first pixel. The stores are device-scope (store16_wt): 24.5 us per launch on the
+    // 64 x 3 x 224 x 224 stem against 25.7 with stores that leave dirty L2 lines to be written back at the end of the
+    // launch (64-byte runs). Runs of 128 bytes, so each store writes whole lines instead of halves whose other half
+    // comes from another wave's block: 24.96 against 25.79 us (same process, 16 alternating batches).
+    auto flush = [&](int px0) {
+      u32x4 v[NS];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = r_base[t * 64];
-      const int p0 = blk * 32 + 8 * (lane & 3);  // the lane's 8 pixels of one output row (out_w % 8 == 0)
+      for (int t = 0; t < NS; ++t) v[t] = WIDE ? r_base[t & 1][t * 64] : r_base[0][t * 64];  // + 1 KiB per read
+      const int p0 = px0 + 8 * (lane & (WIDE ? 7 : 3));  // the lane's 8 pixels of one output row (out_w % 8 == 0)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < NS; ++t) {
         const int voff = p0 < p_end && f_ok[t] ? y_tile + f_off[t] + p0 * 2 : kOut;
         store16_wt(yr, voff, v[t]);
       }
     };
-    for (int ba = wave; ba < g.NB; ba += 2 * kStCW) {
-      const int bb = ba + kStCW;
-      uint32_t d[KS][4];
-      f32x16 acc0, acc1;
-      load(ba, d);
-      multiply(d, acc0, acc1);
-      if (bb < g.NB) {
-        load(bb, d);
-        store(ba, acc0, acc1);
+    if constexpr (WIDE) {
+      // wave w takes the block pairs (2p, 2p + 1), p = w, w + 7, ...: the second block's rows are read before the
+      // first block's tile is staged; both leave together as 128-byte runs
+      for (int pk = wave; 2 * pk < g.NB; pk += kStCW) {
+        const int ba = 2 * pk, bb = ba + 1;
+        uint32_t d[KS][4];
+        f32x16 acc0, acc1;
+        load(ba, d);
         multiply(d, acc0, acc1);
-        store(bb, acc0, acc1);
-      } else {
-        store(ba, acc0, acc1);
+        if (bb < g.NB) {
+          load(bb, d);
+          stage(0, acc0, acc1);
+          multiply(d, acc0, acc1);
+          stage(1, acc0, acc1);
+        } else {
+          stage(0, acc0, acc1);  // the second half's pixels are past the tile: never stored
+        }
+        flush(ba * 32);
+      }
+    } else {
+      // blocks in pairs (wave, wave + 7), (wave + 14, wave + 21), ...: the second block's rows are read before the
+      // first block's stores are issued
+      for (int ba = wave; ba < g.NB; ba += 2 * kStCW) {
+        const int bb = ba + kStCW;
+        uint32_t d[KS][4];
+        f32x16 acc0, acc1;
+        load(ba, d);
+        multiply(d, acc0, acc1);
+        if (bb < g.NB) {
+          load(bb, d);
+          stage(0, acc0, acc1);
+          flush(ba * 32);
+          multiply(d, acc0, acc1);
+          stage(0, acc0, acc1);
+          flush(bb * 32);
+        } else {
+          stage(0, acc0, acc1);
+          flush(ba * 32);
+        }
       }
     }
     stage_barrier();  // tile i's rows are no longer read; tile i+1's have landed
@@ -369,7 +427,9 @@ int stem_prepare(const gie_conv_geom* gg, int cus, StemGeom* g, int* lds, int ma
   const long long grid = 1LL * g->G * ((g->O + 63) / 64);
   if (grid >= (1LL << 31)) return GIE_HIP_EUNSUPPORTED;
   g->tile_off = g->rows_off + kStBufs * g->buf_bytes;
-  if (lds) *lds = g->tile_off + kStCW * 4096;
+  // 128-byte output runs where the LDS holds an 8 KiB tile per multiplying wave
+  g->wide = g->tile_off + kStCW * 8192 <= kStLdsMax ? 1 : 0;
+  if (lds) *lds = g->tile_off + kStCW * (g->wide ? 8192 : 4096);
   return GIE_HIP_OK;
 }
 
@@ -380,22 +440,27 @@ using StemFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint1
 // counts. That form is never instantiated.
 constexpr bool stem_two_rows_only(bool bf16, int c, bool relu) { return bf16 && c == 4 && relu; }
 
-template <typename E, int R, bool RELU>
+template <typename E, int R, bool RELU, bool WIDE>
 StemFn stem_fn(int c) {
   switch (c) {
-    case 1: return &stem_kernel<E, 1, R, RELU>;
-    case 2: return &stem_kernel<E, 2, R, RELU>;
-    case 3: return &stem_kernel<E, 3, R, RELU>;
+    case 1: return &stem_kernel<E, 1, R, RELU, WIDE>;
+    case 2: return &stem_kernel<E, 2, R, RELU, WIDE>;
+    case 3: return &stem_kernel<E, 3, R, RELU, WIDE>;
     default:
       if constexpr (R == 4 && stem_two_rows_only(E::kDtype == GIE_HIP_BF16, 4, RELU)) return nullptr;
-      else return &stem_kernel<E, 4, R, RELU>;
+      else return &stem_kernel<E, 4, R, RELU, WIDE>;
   }
 }
 
-template <typename E>
+template <typename E, bool WIDE>
 StemFn stem_fn(int c, int r, bool relu) {
-  if (r == 4) return relu ? stem_fn<E, 4, true>(c) : stem_fn<E, 4, false>(c);
-  return relu ? stem_fn<E, 2, true>(c) : stem_fn<E, 2, false>(c);
+  if (r == 4) return relu ? stem_fn<E, 4, true, WIDE>(c) : stem_fn<E, 4, false, WIDE>(c);
+  return relu ? stem_fn<E, 2, true, WIDE>(c) : stem_fn<E, 2, false, WIDE>(c);
+}
+
+template <typename E>
+StemFn stem_fn(int c, int r, bool relu, bool wide) {
+  return wide ? stem_fn<E, true>(c, r, relu) : stem_fn<E, false>(c, r, relu);
 }
 
 }  // namespace
@@ -422,7 +487,8 @@ extern "C" int gie_hip_conv_stem(int dtype, const gie_conv_geom* gg, const void*
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
       (reinterpret_cast<uintptr_t>(y) & 15u))
     return GIE_HIP_EUNSUPPORTED;
-  const StemFn fn = bf ? stem_fn<Bf16>(g.C, g.R, gg->relu != 0) : stem_fn<Fp16>(g.C, g.R, gg->relu != 0);
+  const StemFn fn = bf ? stem_fn<Bf16>(g.C, g.R, gg->relu != 0, g.wide != 0)
+                       : stem_fn<Fp16>(g.C, g.R, gg->relu != 0, g.wide != 0);
   if (fn == nullptr) return GIE_HIP_EUNSUPPORTED;
   if (int rc = set_lds_limit(reinterpret_cast<const void*>(fn), lds)) return rc;
   const unsigned grid = unsigned(g.G * ((g.O + 63) / 64));
