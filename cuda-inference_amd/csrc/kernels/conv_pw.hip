@@ -232,7 +232,7 @@ __global__ __launch_bounds__(kPwNT, 2) void pw_kernel(const uint16_t* __restrict
 // and an X slice from L2 for every 128 x 128 output tile, and its 2 x 2 MFMA blocks per wave need ~256 B/clk of
 // LDS reads at the MFMA rate (more than the LDS delivers). Here one workgroup per CU (8 waves, two per SIMD) keeps
 // 256 filters x all C input channels in VGPRs for its whole life and streams one contiguous range of 64-pixel
-// blocks of the flattened B*H*W pixel axis through a four-stage LDS ring:
+// blocks of the flattened B*H*W pixel axis through a three-stage LDS ring:
 //   * the weights come in once per workgroup: 256 filters x C by LDS-DMA into the LDS the ring and the output
 //     tiles use later, each filter's OIHW row as 16-byte slots permuted by the filter index (kc ^ (f % RC)), so the
 //     loads read whole rows and every wave's B-operand reads (filters 64*(w%4) .. +63, W[o][16j + 8*(lane/32) ..])
@@ -242,18 +242,23 @@ __global__ __launch_bounds__(kPwNT, 2) void pw_kernel(const uint16_t* __restrict
 //   * wave w takes pixel half w/4 against its 64 filters: A fragments by ds_read_b64_tr_b16 (rows k..k+3 of a
 //     16-lane group are 64 bytes apart, the two groups of a half-wave 32 bytes: no bank conflicts), 2 MFMA chains;
 //     the bias enters as one more k-step (A = 1 at k = 0, B = bias), after the real ones;
-//   * the epilogue of block i runs spread over the k-steps of block i+1 (two accumulator sets): ReLU + one
-//     rounding, the 64 x 32 tile into the wave's own 4 KiB LDS tile, then 16-byte stores of whole 64-byte rows.
+//   * epilogue: ReLU + one rounding; the two waves of a SIMD (same 64 filters, the two pixel halves) run half a
+//     block apart and put their 64 x 32 halves into one 64 x 64 LDS tile of the block, and the second of them writes
+//     the tile as 16-byte stores of 128-byte runs (8 filter rows per instruction): 34.7-35.1 us against 35.1-37.4
+//     for each wave storing its own half as 64-byte runs with a four-stage ring (config 3, same process,
+//     alternating batches, two boxes), although the 128-byte runs, 32 bytes into a line in three planes out of four
+//     (784-pixel planes), write 1.05x the bytes of the 64-byte ones.
 // Only X travels from L2 to LDS per block. The loads into the ring and the stores are issued through inline
 // assembly in a fixed order so the waits can count them (vmcnt counts both, in issue order). The workgroups that
 // share a pixel range (the 256-filter blocks of O) sit on one XCD (slot L -> XCD L % 8), so each X block comes
 // from HBM once.
 constexpr int kSwO = 256;   // filters per workgroup
 constexpr int kSwP = 64;    // pixels per block (two halves of 32)
-constexpr int kSwNST = 4;   // LDS ring stages
+constexpr int kSwNST = 3;   // LDS ring stages
 constexpr int kSwNW = 8;    // waves
 constexpr int kSwNT = kSwNW * 64;
-constexpr int kSwTile = 4096;  // per-wave output tile (64 filters x 32 pixels x 2 B)
+constexpr int kSwTile = 8192;  // output tile of one filter group and block: 64 filters x 64 pixels x 2 B
+constexpr int kSwTiles = 4 * 2 * kSwTile;  // four filter groups, two tiles each (block parity)
 
 struct PwsGeom {
   int C, HW, O, N;     // N = B*H*W pixels
@@ -321,12 +326,12 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
   constexpr int HB = KS * 1024;           // bytes per pixel half of a stage: 16*KS channels x 32 pixels x 2 B
   constexpr int SB = 2 * HB;              // bytes per stage
   constexpr int WL = KS * 8 * 1024 / (kSwNW * 1024);  // 1 KiB weight units per wave (256 x 16KS x 2 B in all)
-  constexpr int ST_W = 4;                 // stores per wave per block
+  constexpr int ST_W = 8;                 // stores per block of a pixel-half-1 wave (half 0 stores none)
   constexpr int NST = kSwNST;
   constexpr int W_OFF = SB;               // weights land on stages 1 .. NST-1 and the output tiles
   constexpr bool kBf = E::kDtype == GIE_HIP_BF16;
   static_assert(KS == 4 || KS == 8 || KS == 16, "16-channel k-steps");
-  static_assert((NST - 1) * SB + kSwNW * kSwTile >= KS * 8 * 1024, "the weights fit the space they are staged in");
+  static_assert((NST - 1) * SB + kSwTiles >= KS * 8 * 1024, "the weights fit the space they are staged in");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -439,19 +444,18 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
 
   // Ring load D(i+1) has landed for this wave once at most (loads issued after it) remain: the later ring loads
   // (NST-2 blocks) and the store batches issued since. Block j's ring load goes out during the MFMAs of block
-  // j-NST+1; pixel half 0 stores block j after its MFMAs, pixel half 1 stores block j-1 before them, so at the end
-  // of block i that is min(i + 1, NST - 1) or min(i, NST - 2) store batches.
+  // j-NST+1; pixel half 1 stores block j-1 (both halves) before the MFMAs of block j and pixel half 0 stores nothing,
+  // so at the end of block i that is min(i, NST - 2) store batches for half 1, none for half 0.
   auto wait_next = [&](int i) {
     static_assert(NST >= 3 && NST <= 6, "wait_next enumerates the warm-up blocks of a 3- to 6-stage ring");
-    const int k = ph == 0 ? (i + 1 < NST - 1 ? i + 1 : NST - 1) : (i < NST - 2 ? i : NST - 2);
+    const int k = ph == 0 ? 0 : (i < NST - 2 ? i : NST - 2);
     if (k == 0) wait_vm<KL * (NST - 2)>();
     else if (k == 1) wait_vm<KL * (NST - 2) + ST_W * 1>();
-    else if (k == 2) wait_vm<KL * (NST - 2) + ST_W * (2 < NST - 1 ? 2 : NST - 1)>();
-    else if (k == 3) wait_vm<KL * (NST - 2) + ST_W * (3 < NST - 1 ? 3 : NST - 1)>();
-    else if (k == 4) wait_vm<KL * (NST - 2) + ST_W * (4 < NST - 1 ? 4 : NST - 1)>();
-    else wait_vm<KL * (NST - 2) + ST_W * (NST - 1)>();
+    else if (k == 2) wait_vm<KL * (NST - 2) + ST_W * (2 < NST - 2 ? 2 : NST - 2)>();
+    else if (k == 3) wait_vm<KL * (NST - 2) + ST_W * (3 < NST - 2 ? 3 : NST - 2)>();
+    else wait_vm<KL * (NST - 2) + ST_W * (NST - 2)>();
   };
-  static_assert(KL * (NST - 2) + ST_W * (NST - 1) < 64, "vmcnt range");
+  static_assert(KL * (NST - 2) + ST_W * (NST - 2) < 64, "vmcnt range");
 
   // The bias enters as one more MFMA k-step after the real ones: A = 1 at k = 0 for every pixel, B = bias at
   // k = 0 for the lane's filter (lanes 0-31 carry k = 0..7). The single non-zero product is exact, so the sum is
@@ -460,37 +464,40 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
   const u32x4 a_one = lane < 32 ? u32x4{one, 0u, 0u, 0u} : u32x4{0u, 0u, 0u, 0u};
   const u32x4 b_bias[2] = {u32x4{braw[0] & 0xffffu, 0u, 0u, 0u}, u32x4{braw[1] & 0xffffu, 0u, 0u, 0u}};
 
-  // ---- epilogue of the previous block, spread over the k-steps of the current one ----
-  // The accumulators hold, per lane, filter o_lane[nb] and pixels 8q + 4*(lane/32) + 0..3 of the wave's half.
-  // They go through the wave's LDS tile [64 filters][32 pixels] (64-byte rows, the 8-byte granule g of row r at
-  // g ^ ((r/4) & 7), so the granule writes of 32 rows and the 16-byte row reads are free of bank conflicts) and
-  // leave as 16-byte stores of 16 whole 64-byte rows per instruction.
-  const unsigned stg = lds0 + unsigned(NST * SB) + unsigned(wave) * kSwTile;
+  // ---- epilogue: both pixel halves of a block leave together, as 128-byte runs ----
+  // The accumulators hold, per lane, filter o_lane[nb] and pixels 8q + 4*(lane/32) + 0..3 of the wave's half. The two
+  // waves of a filter group (w and w+4, one SIMD) write their halves into the group's tile of the block: [64 filters]
+  // [64 pixels], 128-byte rows, the 16-byte segment s of row r (pixels 8s .. 8s+7) at s ^ ((r / 2) & 7), so the 8-byte
+  // writes of 32 rows see 2-way bank conflicts and the 16-byte row reads none. Half 0 writes block i's half after its
+  // MFMAs; half 1 writes block i's half at the start of block i+1 (after the barrier that follows half 0's writes),
+  // reads the whole tile and stores it, 8 lanes per 128-byte run of a filter's output row, 8 rows per store
+  // instruction. Each group has a tile per block parity: half 0 writes block i+1's tile while half 1 still reads
+  // block i's, and block i+2 reuses block i's tile only after the barrier that ends block i+1.
+  const unsigned stg = lds0 + unsigned(NST * SB) + unsigned(fg) * 2u * unsigned(kSwTile);
   typedef __attribute__((address_space(3))) u32x2 lds_u32x2_t;
   typedef __attribute__((address_space(3))) const u32x4 lds_cu32x4_t;
-  // Tile layout: row r (64 bytes) holds filter 64fg + r; its 8-byte granule g sits at g ^ (2 * ((r / 4) & 3)).
-  // Granule writes (q, nb): row 32nb + lane%32, granule 2q + lane/32; the swizzle keeps granule pairs together, so
-  // a 16-byte segment s of row r is the 16-byte chunk s ^ ((r / 4) & 3) (2-way bank conflict on the writes, none
-  // on the reads).
-  lds_u32x2_t* w_q[4];
+  lds_u32x2_t* w_q[4];  // granule writes (q, nb): row 32nb + lane%32, segment 4ph + q, 8-byte half lane/32
   {
-    const unsigned f = (unsigned(lane) >> 2) & 3u, h = unsigned(lane) >> 5;
+    const unsigned r = unsigned(lane) & 31u, m = (r >> 1) & 7u, h = unsigned(lane) >> 5;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      w_q[q] = reinterpret_cast<lds_u32x2_t*>(size_t(stg + unsigned(lane & 31) * 64u + (((unsigned(q) ^ f) << 1 | h) << 3)));
+      w_q[q] = reinterpret_cast<lds_u32x2_t*>(size_t(stg + r * 128u + (((4u * unsigned(ph) + unsigned(q)) ^ m) << 4) + (h << 3)));
   }
-  // row read t covers rows 16t + lane/4 ((r / 4) & 3 = (lane / 16) & 3 for every t), 16-byte segment lane%4
-  lds_cu32x4_t* const r_base = reinterpret_cast<lds_cu32x4_t*>(
-      size_t(stg + (unsigned(lane) >> 2) * 64u + (((unsigned(lane) & 3u) ^ ((unsigned(lane) >> 4) & 3u)) << 4)));
-  // y offset of the row of read t: filter o0 + 64fg + 16t + lane/4 (y_bytes past O: out of range)
-  unsigned o_row[4];
+  // row read t covers rows 8t + lane/8, segment lane%8, stored at (lane%8) ^ (lane/16 + 4 (t%2))
+  lds_cu32x4_t* r_base[2];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int o = o0 + 64 * fg + 16 * t + (lane >> 2);
+  for (int par = 0; par < 2; ++par)
+    r_base[par] = reinterpret_cast<lds_cu32x4_t*>(size_t(
+        stg + (unsigned(lane) >> 3) * 128u + (((unsigned(lane) & 7u) ^ ((unsigned(lane) >> 4) + 4u * unsigned(par))) << 4)));
+  // y offset of the row of read t: filter o0 + 64fg + 8t + lane/8 (y_bytes past O: out of range)
+  unsigned o_row[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int o = o0 + 64 * fg + 8 * t + (lane >> 3);
     o_row[t] = o < g.O ? unsigned(o) * hw * 2u : unsigned(g.y_bytes);
   }
-  const unsigned d_y = 32u * unsigned(ph) + 8u * unsigned(lane & 3);  // the lane's first pixel of a row segment
-  unsigned st_x = 0;                                                   // y offset of that pixel
+  const unsigned d_y = 8u * unsigned(lane & 7);  // the lane's first pixel of a row segment
+  unsigned st_x = 0;                            // y offset of that pixel
   auto seg_offset = [&](int i, const Base& bb) {
     if (bb.whole) {
       st_x = (bb.b0 * unsigned(g.O) * hw + bb.p0) * 2u + d_y * 2u;
@@ -503,7 +510,7 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
       st_x = sel_or_out(n < unsigned(g.N), (b * unsigned(g.O) * hw + p) * 2u);
     }
   };
-  auto put = [&](const f32x16 (&acc)[2], int q, int nb) {
+  auto put = [&](const f32x16 (&acc)[2], int q, int nb, int par) {
     uint32_t h[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -515,22 +522,27 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
       h[e] = pack2<E>(v0, v1);
       if (RELU && !kBf) h[e] = relu2<E>(h[e]);
     }
-    w_q[q][nb * 256] = u32x2{h[0], h[1]};  // + 2048 bytes for the second 32-filter block
+    w_q[q][nb * 512 + par * 1024] = u32x2{h[0], h[1]};  // + 32 rows for the second 32-filter block, + 8 KiB per parity
   };
-  auto epilogue = [&](const f32x16 (&acc)[2], int i) {
-    seg_offset(i, base_of(i));
+  auto stage_half = [&](const f32x16 (&acc)[2], int i) {
+    const int par = i & 1;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) put(acc, q, nb);
+      for (int nb = 0; nb < 2; ++nb) put(acc, q, nb, par);
     // A wave's LDS accesses complete in issue order, so the reads see the writes once the compiler keeps that order
     // (the tile is written as 8-byte and read as 16-byte vectors, which type-based alias analysis would separate).
     asm volatile("" ::: "memory");
-    u32x4 v[4];
+  };
+  auto epilogue = [&](const f32x16 (&acc)[2], int i) {  // pixel half 1: its half of block i, then the block to y
+    seg_offset(i, base_of(i));
+    stage_half(acc, i);
+    const int par = i & 1;
+    u32x4 v[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) v[t] = r_base[t * 64];  // + 1024 bytes per 16 rows
+    for (int t = 0; t < 8; ++t) v[t] = r_base[t & 1][t * 64 + par * 512];  // + 1 KiB per 8 rows, + 8 KiB per parity
 #pragma unroll
-    for (int t = 0; t < 4; ++t) store16(yr, int(st_x + o_row[t]), v[t]);
+    for (int t = 0; t < 8; ++t) store16(yr, int(st_x + o_row[t]), v[t]);
   };
 
   // ---- A-fragment addresses: 16-lane group g16 reads pixels 16*(g16&1) .. +15 of channel rows k0 .. k0+3,
@@ -579,7 +591,7 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
   for (int i = 0; i < nblk; ++i) {
     if (ph == 1 && i > 0) epilogue(acc, i - 1);
     compute(i);
-    if (ph == 0) epilogue(acc, i);
+    if (ph == 0) stage_half(acc, i);
     wait_next(i);  // block i+1 has landed (this wave's part)
     stage_barrier();
   }
@@ -687,7 +699,7 @@ extern "C" int gie_hip_pws_check(const gie_conv_geom* g, int* lds_bytes) {
   PwsGeom pg;
   int ks = 0;
   const int rc = pws_prepare(g, 256, &pg, &ks);
-  if (rc == GIE_HIP_OK && lds_bytes) *lds_bytes = kSwNST * 2 * ks * 1024 + kSwNW * kSwTile;
+  if (rc == GIE_HIP_OK && lds_bytes) *lds_bytes = kSwNST * 2 * ks * 1024 + kSwTiles;
   return rc;
 }
 
@@ -718,7 +730,7 @@ extern "C" int gie_hip_conv_pws(int dtype, const gie_conv_geom* gg, const void* 
        {{&pws_kernel<Bf16, 16, false, false>, &pws_kernel<Bf16, 16, false, true>},
         {&pws_kernel<Bf16, 16, true, false>, &pws_kernel<Bf16, 16, true, true>}}}};
   const Fn fn = table[dtype == GIE_HIP_BF16 ? 1 : 0][ks == 4 ? 0 : ks == 8 ? 1 : 2][g.relu ? 1 : 0][g.HW >= kSwP ? 1 : 0];
-  const int lds = kSwNST * 2 * ks * 1024 + kSwNW * kSwTile;  // ring + one 4 KiB output tile per wave
+  const int lds = kSwNST * 2 * ks * 1024 + kSwTiles;  // ring + two 8 KiB output tiles per filter group
   if (int rc = set_lds_limit(reinterpret_cast<const void*>(fn), lds)) return rc;
   const long long slots = static_cast<long long>((g.n_ranges + 7) / 8) * 8 * g.n_ob;
   hipLaunchKernelGGL(fn, dim3(unsigned(slots)), dim3(kSwNT), lds, static_cast<hipStream_t>(stream),

@@ -74,7 +74,8 @@ def test_pointwise_streaming_kernel_through_cabi(case):
     g = p.geom(p.in_channels)
     lds = ctypes.c_int(0)
     assert gie.hip().gie_hip_pws_check(ctypes.byref(g), ctypes.byref(lds)) == 0
-    assert lds.value in (4 * 8192 + 32768, 4 * 16384 + 32768, 4 * 32768 + 32768)  # ring + 4 KiB output tile per wave
+    # a three-stage ring + two 8 KiB output tiles per filter group
+    assert lds.value in (3 * 8192 + 65536, 3 * 16384 + 65536, 3 * 32768 + 65536)
     for rep in range(2):  # the second launch overwrites the first's output with the same bits
         b.t.poison()
         gie.check_hip(gie.hip().gie_hip_conv_pws(gie.PRECISIONS[case[5]], ctypes.byref(g), b.t.dx.addr,
