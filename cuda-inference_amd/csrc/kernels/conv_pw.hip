@@ -247,7 +247,8 @@ __global__ __launch_bounds__(kPwNT, 2) void pw_kernel(const uint16_t* __restrict
 //     the tile as 16-byte stores of 128-byte runs (8 filter rows per instruction): 34.7-35.1 us against 35.1-37.4
 //     for each wave storing its own half as 64-byte runs with a four-stage ring (config 3, same process,
 //     alternating batches, two boxes), although the 128-byte runs, 32 bytes into a line in three planes out of four
-//     (784-pixel planes), write 1.05x the bytes of the 64-byte ones.
+//     (784-pixel planes), write 1.05x the bytes of the 64-byte ones. The stores are device-scope (store16_wt): 34.77
+//     against 35.17 us with write-back stores (which had won with 64-byte runs).
 // Only X travels from L2 to LDS per block. The loads into the ring and the stores are issued through inline
 // assembly in a fixed order so the waits can count them (vmcnt counts both, in issue order). The workgroups that
 // share a pixel range (the 256-filter blocks of O) sit on one XCD (slot L -> XCD L % 8), so each X block comes
@@ -542,7 +543,7 @@ __global__ __launch_bounds__(kSwNT, 1) void pws_kernel(const uint16_t* __restric
 #pragma unroll
     for (int t = 0; t < 8; ++t) v[t] = r_base[t & 1][t * 64 + par * 512];  // + 1 KiB per 8 rows, + 8 KiB per parity
 #pragma unroll
-    for (int t = 0; t < 8; ++t) store16(yr, int(st_x + o_row[t]), v[t]);
+    for (int t = 0; t < 8; ++t) store16_wt(yr, int(st_x + o_row[t]), v[t]);
   };
 
   // ---- A-fragment addresses: 16-lane group g16 reads pixels 16*(g16&1) .. +15 of channel rows k0 .. k0+3,
