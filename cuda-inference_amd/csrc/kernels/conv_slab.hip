@@ -54,6 +54,7 @@ struct SlabGeom {
   int x_bytes, w_bytes;
   int relu, split;
   int y_vec;                   // outputs leave as 4-byte pixel pairs
+  int y_stage;                 // split form: the unit's output run is staged in LDS and leaves as 16-byte stores
   long long total;             // |Y| elements (partial stride)
   float inv_hw, inv_w;         // 1 / HW, 1 / W for fdiv
   // unit = ((z * rad[2] + d2) * rad[1] + d1) * rad[0] + d0 with d1 = slab; order 0: d0 = filter block, d2 = image
@@ -77,7 +78,7 @@ __device__ __forceinline__ void args_in_sgprs(const void* x, const void* w, cons
   asm volatile("" ::"s"(g.n_units), "s"(g.per_xcd), "s"(g.order), "s"(g.rad[0]), "s"(g.rad[1]), "s"(g.rad[2]),
                "s"(g.mg[0]), "s"(g.mg[1]), "s"(g.mg[2]), "s"(g.sh[0]), "s"(g.sh[1]), "s"(g.sh[2]));
   asm volatile("" ::"s"(g.S), "s"(g.split), "s"(g.C), "s"(g.H), "s"(g.W), "s"(g.HW), "s"(g.O), "s"(g.x_bytes),
-               "s"(g.w_bytes), "s"(g.relu), "s"(g.y_vec), "s"(g.total));
+               "s"(g.w_bytes), "s"(g.relu), "s"(g.y_vec), "s"(g.y_stage), "s"(g.total));
 }
 __device__ __forceinline__ SlabUnit decode_unit(int unit, const SlabGeom& g) {
   const int q0 = magic_div(unit, g.mg[0], g.sh[0]), d0 = unit - q0 * g.rad[0];
@@ -181,6 +182,31 @@ __device__ __forceinline__ void round_pairs(const f32x4& out, const float (&bv)[
   *wb = (wb_o & oddm) | (wb_e & ~oddm);
 }
 
+// The pixel-pair words of one 16-position output row (one row per block, P == 16): bias + ReLU + one rounding of the
+// lane's four filters with two packed conversions, then two selects, one lane-pair swap and two byte permutes. Word a
+// holds filter fp's values at columns (c, c + 1), word b filter fp + 1's (even lane: fp = 0 and c its column; odd
+// lane: fp = 2 and c its column - 1).
+struct PairSel {
+  uint32_t odd, sel_a, sel_b;
+  __device__ __forceinline__ explicit PairSel(int lane)
+      : odd(uint32_t(lane & 1)), sel_a(odd ? 0x01000504u : 0x05040100u), sel_b(odd ? 0x03020706u : 0x07060302u) {}
+};
+template <typename E, bool RELU>
+__device__ __forceinline__ void row_pairs(const f32x4& out, const float (&bv)[4], const PairSel& ps, uint32_t* wa,
+                                          uint32_t* wb) {
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float t = out[i] + bv[i];
+    v[i] = RELU ? fmaxf(t, 0.0f) : t;
+  }
+  const uint32_t h01 = E::pack2(v[0], v[1]), h23 = E::pack2(v[2], v[3]);
+  const uint32_t send = ps.odd ? h01 : h23, mine = ps.odd ? h23 : h01;
+  const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap lane pairs
+  *wa = __builtin_amdgcn_perm(recv, mine, ps.sel_a);
+  *wb = __builtin_amdgcn_perm(recv, mine, ps.sel_b);
+}
+
 template <typename E, int P, int NBW, bool PADS_LOADED = false>
 __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uint32_t (&bbits)[4], int lane, int wr,
                                            int oh0, int nrows, int b, int z, int o0, int f0,
@@ -220,12 +246,10 @@ __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uin
   if constexpr (PADS_LOADED && P == 16) {
     if (g.y_vec) {
       // one 16-position block per output row: block j is row wr * RW + j, the lane's column is lane % 16. Pixel
-      // pairs as below, built with two packed conversions, two selects, one lane-pair swap and two byte permutes;
-      // the store offsets are a per-lane base (kOut for a column or filter outside the output) plus a wave-uniform
-      // row displacement, and rows past the slab's end are skipped by a uniform branch.
-      const uint32_t odd = uint32_t(lane & 1);
-      const int fp = int(odd) * 2, col = (lane & 15) - int(odd);
-      const uint32_t sel_a = odd ? 0x01000504u : 0x05040100u, sel_b = odd ? 0x03020706u : 0x07060302u;
+      // pairs by row_pairs; the store offsets are a per-lane base (kOut for a column or filter outside the output)
+      // plus a wave-uniform row displacement, and rows past the slab's end are skipped by a uniform branch.
+      const PairSel ps(lane);
+      const int fp = int(ps.odd) * 2, col = (lane & 15) - int(ps.odd);
       const int row0 = oh0 + wr * RW;
       const bool lane_ok = col < g.W && fp < nf;
       const int base = lane_ok ? (fbase + fp * g.HW + row0 * g.W + col) * 2 : kOut;
@@ -234,18 +258,10 @@ __device__ __forceinline__ void slab_store(const f32x4 (&acc)[3][NBW], const uin
 #pragma unroll
         for (int j = 0; j < NBW; ++j) {
           if (wr * RW + j >= nrows) break;
-          const f32x4 out = column(j);
-          float v[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float t = out[i] + bv[i];
-            v[i] = decltype(relu_c)::value ? fmaxf(t, 0.0f) : t;
-          }
-          const uint32_t h01 = E::pack2(v[0], v[1]), h23 = E::pack2(v[2], v[3]);
-          const uint32_t send = odd ? h01 : h23, mine = odd ? h23 : h01;
-          const uint32_t recv = uint32_t(__builtin_amdgcn_mov_dpp(int(send), 0xB1, 0xf, 0xf, false));  // swap pairs
-          store4s(yr, base, 2 * j * g.W, __builtin_amdgcn_perm(recv, mine, sel_a));
-          store4s(yr, base, 2 * (j * g.W + g.HW), __builtin_amdgcn_perm(recv, mine, sel_b));
+          uint32_t wa, wb;
+          row_pairs<E, decltype(relu_c)::value>(column(j), bv, ps, &wa, &wb);
+          store4s(yr, base, 2 * j * g.W, wa);
+          store4s(yr, base, 2 * (j * g.W + g.HW), wb);
         }
       };
       if (g.relu) rows(std::true_type{});
@@ -1100,6 +1116,48 @@ struct SplitShare {
   }
 };
 
+// Staged epilogue of the split form (g.y_stage: whole images per unit, O % 32 == 0, 16-byte aligned y, P == 16). The
+// unit's 32 output planes are one contiguous run of 64 * HW bytes; the multiplying waves write their pixel pairs at
+// their places in that run into an LDS activation stage that no load targets any more, and after one barrier all eight
+// waves write the run with 16-byte device-scope stores (store16_wt), each store instruction one contiguous kilobyte of
+// y, so whole lines are written through the L2 and none is left dirty for the end of the launch (the direct
+// pixel-pair stores spread every instruction over eight filter planes in 28-byte pieces).
+// Lanes past the last column write their pairs to a dummy area after the run (inside the stage), so no lane is masked.
+template <typename E, int NBW>
+__device__ __forceinline__ void split_stage_rows(const f32x4 (&acc)[3][NBW], const uint32_t (&bbits)[4], int lane,
+                                                 int wr, int fl, int nrows, unsigned stg, const SlabGeom& g) {
+  constexpr int RW = NBW;  // P == 16: one output row per 16-position block
+  float bv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bv[i] = E::to_f32(uint16_t(bbits[i]));
+  const PairSel ps(lane);
+  const int fp = int(ps.odd) * 2, col = (lane & 15) - int(ps.odd);
+  const unsigned plane = unsigned(2 * g.HW);
+  const unsigned base = stg + (col < g.W ? unsigned(((fl + fp) * g.HW + wr * RW * g.W + col) * 2) : 32u * plane);
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
+  auto rows = [&](auto relu_c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      if (wr * RW + j >= nrows) break;
+      uint32_t wa, wb;
+      row_pairs<E, decltype(relu_c)::value>(slab_column<16, NBW, true>(acc, j, lane, wr, g.W), bv, ps, &wa, &wb);
+      const unsigned a = base + unsigned(2 * j * g.W);
+      *reinterpret_cast<lds_u32*>(size_t(a)) = wa;
+      *reinterpret_cast<lds_u32*>(size_t(a + plane)) = wb;
+    }
+  };
+  if (g.relu) rows(std::true_type{});
+  else rows(std::false_type{});
+}
+
+// The staged run of 64 * HW bytes (4 * HW 16-byte chunks) from LDS to y, by the workgroup's 512 threads.
+__device__ __forceinline__ void split_copy_out(unsigned stg, uint16_t* __restrict__ y, int b, int o0, int tid,
+                                               const SlabGeom& g) {
+  const int n16 = 4 * g.HW;
+  const v4i yr = make_vsharp(y + static_cast<long long>(b * g.O + o0) * g.HW, 16 * n16);
+  for (int c = tid; c < n16; c += 512) store16_wt(yr, 16 * c, rd16(stg + unsigned(16 * c)));
+}
+
 template <typename E, int P, int NBW, int NST>
 __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ w,
@@ -1155,6 +1213,12 @@ __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __re
       stage_barrier();
     }
     wait_vmcnt<0>();  // the zero loads past the last slice land before this wave ends
+    if constexpr (P == 16) {
+      if (g.y_stage) {
+        stage_barrier();  // the multiplying waves' rows are in LDS
+        split_copy_out(lds0 + unsigned(((ns - 1) % NST) * ACT), y, b, o0, tid, g);
+      }
+    }
     return;
   }
 
@@ -1259,6 +1323,17 @@ __global__ __launch_bounds__(512, 1) void slab_split_kernel(const uint16_t* __re
   wait_vmcnt<0>();  // the bias loads
 #pragma unroll
   for (int i = 0; i < 4; ++i) touch_v(bbits[i]);
+  if constexpr (P == 16) {
+    if (g.y_stage) {
+      // slice ns - 1's stage: its last load landed before step ns - 2, its last reads were in step ns - 2, and the
+      // loads past the last slice (slices ns, ns + 1) target the other two stages
+      const unsigned stg = lds0 + unsigned(((ns - 1) % NST) * ACT);
+      split_stage_rows<E, NBW>(acc, bbits, lane, wr, f0 - o0, nrows, stg, g);
+      stage_barrier();  // every wave's rows are in LDS
+      split_copy_out(stg, y, b, o0, tid, g);
+      return;
+    }
+  }
   slab_store<E, P, NBW, true>(acc, bbits, lane, wr, oh0, nrows, b, z, o0, f0, y, partial, g);
 }
 
@@ -1315,14 +1390,15 @@ SlabFn pick_fn(bool bf, int mode) {
 }
 
 struct SlabShapeInfo {
-  int P, RB, CS, NT, LDS;
+  int P, RB, CS, NT, LDS, ACT, FORM;
 };
 
 template <int I>
 SlabShapeInfo shape_of() {
   using Sh = typename CfgT<I>::Sh;
   // the split form adds one loader wave per SIMD
-  return SlabShapeInfo{CfgT<I>::P, Sh::RB, Sh::CS, CfgT<I>::FORM == kSplit ? 2 * Sh::NT : Sh::NT, CfgT<I>::LDS};
+  return SlabShapeInfo{CfgT<I>::P,   Sh::RB, Sh::CS, CfgT<I>::FORM == kSplit ? 2 * Sh::NT : Sh::NT, CfgT<I>::LDS,
+                       Sh::ACT, CfgT<I>::FORM};
 }
 
 template <int... Is>
@@ -1410,6 +1486,11 @@ int slab_prepare(int cfg, const gie_conv_geom* gg, int dtype, const void* x, con
   g.inv_w = 1.0f / float(gg->in_w);
   // 4-byte stores of pixel pairs: even rows, so every pair starts on an even element of a 4-byte aligned y
   g.y_vec = split == 1 && gg->in_w % 2 == 0 && !(reinterpret_cast<uintptr_t>(y) & 3u);
+  // staged output (split form): whole images per unit and whole 32-filter blocks, so a unit's 32 output planes are one
+  // run of 64 * HW bytes, 16-byte aligned when y is; the run, plus the dummy words of the lanes past the last column,
+  // fits one activation stage
+  g.y_stage = si.FORM == kSplit && g.y_vec && bands == 1 && g.O % kSlTO == 0 &&
+              !(reinterpret_cast<uintptr_t>(y) & 15u) && 64 * hw + 2 * (1LL * si.RB * gg->in_w + hw) + 4 <= si.ACT;
   sp->fn = fn;
   sp->nt = si.NT;
   sp->lds = si.LDS;

@@ -59,8 +59,9 @@ __device__ __forceinline__ void store16(v4i rsrc, int voff, u32x4 v) {
 
 // store16 at device scope (sc1): the line is written through this XCD's L2 rather than left dirty in it, so a launch
 // that streams its whole output once does not end with the write-back of every dirty L2 line. Whether that pays is
-// a property of the kernel's store stream: measured faster for the stem kernel and for the pointwise kernel's 128-byte
-// runs (slower for its earlier 64-byte runs), slower for the slab kernels' pixel-pair stores, which keep store16.
+// a property of the kernel's store stream: measured faster for the stem kernel, the pointwise kernel's 128-byte runs
+// (slower for its earlier 64-byte runs) and the split slab kernel's staged whole-line output, slower for the slab
+// kernels' scattered pixel-pair stores, which keep store16.
 __device__ __forceinline__ void store16_wt(v4i rsrc, int voff, u32x4 v) {
   asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen sc1\n\ts_nop 1" ::"v"(v), "v"(voff), "s"(rsrc) : "memory");
 }

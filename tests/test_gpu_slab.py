@@ -6,7 +6,8 @@ Cases cover every registered configuration on slabs that are whole images and im
 rows narrower than the pitch, channel counts that are not a multiple of the slice (zero-filled channels), filter
 counts past and below a 32-filter block, each activation load form (4-byte direct-to-LDS loads of even rows of a
 4-byte aligned x, 2-byte loads of odd rows or a 2-byte aligned x),
-pixel-pair and 2-byte output stores, no bias / no ReLU, both precisions, split-K with the reduce kernel, a second launch giving the
+pixel-pair and 2-byte output stores, the split form's LDS-staged 16-byte output stores (whole images, O % 32 == 0,
+16-byte aligned y) against its pixel-pair stores bit for bit, no bias / no ReLU, both precisions, split-K with the reduce kernel, a second launch giving the
 same bits, and argument rejection.
 """
 import ctypes
@@ -147,6 +148,35 @@ def test_slab_bench_config_full_size(cfg_name):
             assert gates["rel_l2"] <= 1e-3 and gates["max_abs"] <= 2e-2, f"config {ci} sk{split}: {gates}"
             ran += 1
     assert ran > 0
+
+
+def _split_config():
+    for ci, cfg in enumerate(_configs()):
+        if cfg.threads == 512:
+            return ci
+    pytest.fail("no split-form slab configuration registered")
+
+
+@pytest.mark.parametrize("shape", [(2, 64, 14, 14, 32, "fp16", True, True), (2, 96, 14, 12, 64, "bf16", True, False),
+                                   (1, 160, 9, 10, 64, "fp16", False, True), (1, 32, 10, 10, 32, "bf16", True, True),
+                                   (32, 256, 14, 14, 256, "fp16", True, True)],
+                         ids=lambda c: "x".join(map(str, c[:5])) + f"-{c[5]}")
+def test_split_staged_output_matches_pixel_pair_stores(shape):
+    """The split form stages a whole-image unit's output in LDS and writes it with 16-byte stores when y is 16-byte
+    aligned; a y 4 bytes off that takes the direct pixel-pair stores. Same accumulators, same rounding: the bits must
+    agree, on two launches each (one slice, three, five, eight: the staging stage follows the slice count)."""
+    B, C, H, W, K, prec, bias, relu = shape
+    p = _problem(B, C, H, W, K, prec, bias, relu)
+    b = Bundle(p, 0x5E7A + C + K, O.NORMAL)
+    ci = _split_config()
+    print(f"split config {ci} on {shape}: staged (y offset 0) and direct (y offset 4)", flush=True)
+    staged = _run(p, b, ci, 1, 0, 0, reps=2)
+    direct = _run(p, b, ci, 1, 0, 4, reps=2)
+    assert staged is not None and direct is not None
+    m = b.compare(staged[0])
+    assert m.passed(), m.summary()
+    for y in staged[1:] + direct:
+        assert np.array_equal(np.nan_to_num(staged[0]), np.nan_to_num(y))
 
 
 def test_slab_argument_checks():
