@@ -28,7 +28,9 @@
 //     register loads and 2-byte LDS writes instead (full form; padding cleared once).
 // Epilogue (slab_store): the DPP shift-add of the three accumulator sets, then bias + ReLU + one RNE rounding (the
 // reference's apply_epilogue order, src/kernels/fused_epilogue.cuh:11-16) and stores straight from the registers:
-// 4-byte pixel pairs (lane pairs exchange halves by DPP) or 2-byte values. split > 1: FP32 partials
+// 4-byte pixel pairs (lane pairs exchange halves by DPP) or 2-byte values; the split form (loader waves) stages the
+// pixel pairs of a whole-image unit in LDS instead and writes its 32 planes as one run of 16-byte device-scope stores
+// (split_stage_rows, split_copy_out). split > 1: FP32 partials
 // partial[z][NCHW] over the z-th range of channel slices [floor(S*z/split), floor(S*(z+1)/split)), the partition of
 // src/kernels/tensor_core_mma.cu:112-115, reduced by splitk_reduce.hip.
 // Grid: units (split range, image, slab, 32-filter block); XCD x (slot mod 8) takes a contiguous range of units, with
