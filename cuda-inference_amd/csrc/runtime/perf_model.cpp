@@ -58,8 +58,9 @@ constexpr FamilyProfile kFamilies[] = {
     {"band_", 0.27, 0.45, 5.0},     // L2 18.9 us including the weight repack launch
     {"halo_", 0.37, 0.40, 10.0},    // L2 23.3 us including the repack launch, L5 24.7 us at split 4
     {"mfma_", 0.22, 0.35, 8.0},     // L2 25.7 us, L3 87 us, L4 145 us, L5 26.0 us at split 4
-    {"pw_", 0.30, 0.48, 2.0},       // L3 37.2 us (weight-stationary streaming form) = 3.5 TB/s of compulsory traffic
-    {"stem_", 0.25, 0.615, 2.0},    // L4 28.3 us = 4.3 TB/s
+    {"pw_", 0.30, 0.48, 2.0},       // L3 37.2-39.6 us (weight-stationary streaming form; shared tiles, 128-byte
+                                    // device-scope runs) = 3.3-3.5 TB/s of compulsory traffic
+    {"stem_", 0.28, 0.69, 2.0},     // L4 26.6-26.8 us (128-byte device-scope output runs) = 4.6 TB/s
     {"narrow_", 0.084, 0.30, 2.0},  // L5 15.0 us (123 TFLOP/s)
     {"stack_", 0.33, 0.40, 4.1},    // L5 9.6 us at split 2 (6.7 conv + 2.8 reduce), 10.2 at split 1
     {"deep_", 0.44, 0.40, 2.9},     // L5 6.6 us: steps at 0.44 of peak, ~4.2 us of set-up, first stage and
